@@ -1,0 +1,251 @@
+"""Benchmark of the quantized linear hot path on one MI355X.
+
+Headline: AQ4 g128 matvec, M=1, K=4096, N=14336,
+bf16 activations, fp32 accumulation, in GB/s of algorithmic HBM traffic
+(N*K/2 + 4*N*K/128 + 2*M*K + 2*M*N bytes per launch).
+
+One "step" is one sweep of forward calls over R rotated weight copies
+(R chosen so the copies total more than 1 GB, defeating the 256 MB Infinity
+Cache), captured once into a HIP graph and replayed, so that the timed region
+holds back-to-back kernels with inputs already resident in HBM.  The kernel's
+average duration is timed with HIP events on the stream the kernels run on.
+
+Extra configurations (FP8 matvec, the small-M sweep, the M=2048 FP8 GEMM and
+the 32-layer AQ4 decode stack) are reported under "configs".  The CPU
+baseline is this build's own C restatement (oracle/), not a reference CPU
+path: the reference has none.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs a,b]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "ullm-project_amd"))
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5030.0  # dense, 256 CU x 2.4 GHz x 8192 flop/clk/CU
+ROTATE_BYTES = 1 << 30
+
+
+def fp8_bytes(m, n, k):
+    return n * k + 4 * n + 2 * m * k + 2 * m * n
+
+
+def aq4_bytes(m, n, k):
+    return n * k // 2 + 4 * n * k // 128 + 2 * m * k + 2 * m * n
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Creates rotated weight copies and times graph replays of forwards."""
+
+    def __init__(self, uh, torch, device):
+        self.uh = uh
+        self.torch = torch
+        self.dev = device
+        self.stream = torch.cuda.Stream(device=device)
+
+    def weights(self, encoding, n, k, copies, seed=0):
+        torch = self.torch
+        g = torch.Generator(device=self.dev)
+        out = []
+        for i in range(copies):
+            g.manual_seed(seed * 1000 + i)
+            w = torch.randn((n, k), generator=g, device=self.dev,
+                            dtype=torch.float32) * 0.02
+            out.append(self.uh.LinearWeight.quantize(w, encoding))
+            del w
+        torch.cuda.synchronize()
+        return out
+
+    def time_sweep(self, calls, steps, warmup):
+        """calls: list of zero-arg callables issuing one forward each on the
+        current stream.  Returns (ms per step, us per call, timing mode)."""
+        torch = self.torch
+        mode = "graph"
+        with torch.cuda.stream(self.stream):
+            for c in calls:  # first touch outside capture
+                c()
+            self.stream.synchronize()
+            graph = None
+            try:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=self.stream):
+                    for c in calls:
+                        c()
+            except Exception as exc:  # capture unsupported: eager launches
+                log(f"graph capture failed ({exc}); timing eager launches")
+                graph = None
+                mode = "eager"
+                torch.cuda.synchronize()
+
+            def step():
+                if graph is not None:
+                    graph.replay()
+                else:
+                    for c in calls:
+                        c()
+
+            for _ in range(warmup):
+                step()
+            self.stream.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            for _ in range(steps):
+                step()
+            end.record(self.stream)
+            end.synchronize()
+        ms = start.elapsed_time(end)
+        return ms / steps, 1000.0 * ms / (steps * len(calls)), mode
+
+
+def bench_matvec(r, encoding, m, n, k, steps, warmup, seed=0):
+    torch, uh = r.torch, r.uh
+    per = aq4_bytes(m, n, k) if encoding == uh.ENCODING_AQ4_G128 else fp8_bytes(m, n, k)
+    copies = max(4, -(-ROTATE_BYTES // per))
+    ws = r.weights(encoding, n, k, copies, seed)
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(seed + 7)
+    x = torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=r.dev)
+    calls = [(lambda w=w: w.forward(x, y)) for w in ws]
+    ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
+    gbs = per / (us_call * 1e-6) / 1e9
+    for w in ws:
+        w.destroy()
+    return {"m": m, "n": n, "k": k, "bytes_per_launch": per, "copies": copies,
+            "us_per_launch": us_call, "ms_per_step": ms_step, "GB_s": gbs,
+            "frac_hbm": gbs / HBM_PEAK_GBS, "timing": mode}
+
+
+def bench_gemm(r, m, n, k, steps, warmup):
+    torch, uh = r.torch, r.uh
+    ws = r.weights(uh.ENCODING_FP8_E4M3_ROW, n, k, 2, seed=3)
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(11)
+    x = torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16)
+    xq, xs = uh.quantize_activations(x)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=r.dev)
+    torch.cuda.synchronize()
+    calls = [(lambda w=w: w.forward(xq, y, x_scales=xs)) for w in ws]
+    ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
+    tflops = 2.0 * m * n * k / (us_call * 1e-6) / 1e12
+    for w in ws:
+        w.destroy()
+    return {"m": m, "n": n, "k": k, "us_per_launch": us_call,
+            "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
+            "timing": mode}
+
+
+def cpu_baseline(seconds=10.0):
+    """The oracle's AQ4 matvec on the host cores, same shape, bounded time."""
+    import numpy as np
+    from oracle import oracle as orc
+    m, n, k = 1, 14336, 4096
+    threads = min(16, os.cpu_count() or 1)
+    rs = np.random.default_rng(0)
+    w = (rs.standard_normal((n, k)) * 0.02).astype(np.float32)
+    p, s, z = orc.aq4_quantize(w)
+    xb = orc.bf16_from_f32(rs.standard_normal((m, k)).astype(np.float32))
+    orc.aq4_gemv(xb, p, s, z, threads=threads)
+    t0 = time.perf_counter()
+    calls = 0
+    while time.perf_counter() - t0 < seconds:
+        orc.aq4_gemv(xb, p, s, z, threads=threads)
+        calls += 1
+    dt = (time.perf_counter() - t0) / calls
+    return {"value": aq4_bytes(m, n, k) / dt / 1e9, "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{calls} AQ4 matvecs M=1 K=4096 N=14336 "
+                      f"(oracle fp32 loop, OpenMP {threads} threads, "
+                      f"{dt * 1e3:.1f} ms each)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="aq4,fp8,gemm")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build's kernels are "
+              "single-GPU (see DESIGN.md on sharding); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ullm_hip as uh
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    available, _, diag = uh.backend_probe()
+    if not available:
+        raise SystemExit(f"HIP backend unavailable: {diag}")
+    r = Runner(uh, torch, dev)
+    want = set(args.configs.split(","))
+
+    head = bench_matvec(r, uh.ENCODING_AQ4_G128, 1, 14336, 4096, args.steps,
+                        args.warmup)
+    log("aq4 M=1 K=4096 N=14336:", head)
+    configs = {"aq4_m1_k4096_n14336": head}
+    if "fp8" in want:
+        configs["fp8_m1_k4096_n4096"] = bench_matvec(
+            r, uh.ENCODING_FP8_E4M3_ROW, 1, 4096, 4096, args.steps, args.warmup)
+        log("fp8:", configs["fp8_m1_k4096_n4096"])
+    if "sweep" in want:
+        for kk, nn, name in ((4096, 6144, "qkv"), (4096, 4096, "o"),
+                             (4096, 28672, "gate_up"), (14336, 4096, "down")):
+            for m in (1, 2, 4, 8, 16, 32):
+                res = bench_matvec(r, uh.ENCODING_FP8_E4M3_ROW, m, nn, kk,
+                                   max(10, args.steps // 5), 2)
+                configs[f"fp8_sweep_{name}_m{m}"] = res
+                log(name, m, res["GB_s"])
+    if "gemm" in want:
+        configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
+            r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
+        log("gemm:", configs["fp8_gemm_m2048_k4096_n28672"])
+
+    cpu = cpu_baseline(args.cpu_seconds)
+    us = head["us_per_launch"]
+    line = {
+        "metric": "AQ4 g128 matvec HBM throughput (M=1, K=4096, N=14336)",
+        "value": round(head["GB_s"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic: weights N(0,0.02) quantized on device, x ~ N(0,1) bf16",
+        "config": {"workload": "aq4_matvec_m1_k4096_n14336",
+                   "rotated_weight_copies": head["copies"],
+                   "launches_per_step": head["copies"],
+                   "timing": head["timing"]},
+        "roofline": {"bound": "hbm", "achieved": round(head["GB_s"], 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["GB_s"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel_us": round(us, 3)},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

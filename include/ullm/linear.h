@@ -1,0 +1,203 @@
+/*
+ * ullm/linear.h -- quantized linear-layer entry points (gfx950 build).
+ *
+ * The reference has no numerical linear layer: its Backend trait refuses
+ * execution (reference crates/ullm-core/src/backend.rs:5-11,
+ * crates/ullm-hip/src/lib.rs:510-512) and its Matmul descriptor checks shapes
+ * only (crates/ullm-core/src/op.rs:97-113).  These functions are the native
+ * side that HipBackend::execute would call for a Matmul whose B operand is an
+ * FP8-row-scaled or AQ4 weight.  They follow the reference's ABI v1
+ * conventions exactly (reference include/ullm/hip.h, native/hip/src/hip_stub.cpp):
+ *   - every struct starts with {struct_size, abi_version}; a larger
+ *     struct_size is accepted, a smaller one is ULLM_STATUS_INVALID_ARGUMENT
+ *     (hip_stub.cpp:75-78), a wrong version ULLM_STATUS_INVALID_ABI_VERSION
+ *     (hip_stub.cpp:79-82), non-zero reserved words
+ *     ULLM_STATUS_RESERVED_NONZERO (hip_stub.cpp:94-98);
+ *   - the error sink is validated first and reports like the v1 functions;
+ *   - no C++ exception crosses the boundary (hip_stub.cpp:123,134);
+ *   - handles are opaque, identity is checked against a live-handle table and
+ *     a stale handle is ULLM_STATUS_HIP_INVALID_HANDLE
+ *     (native/hip/src/hip_evidence_runtime.hip.cpp:276-303);
+ *   - caller host memory is copied before a function returns and never kept
+ *     (docs/architecture/runtime.md:77).
+ *
+ * Matrix conventions (all row-major, element strides):
+ *   weight W[N][K]  (one output feature per row, K contiguous)
+ *   activation X[M][K], output Y[M][N], Y = alpha * X * W^T.
+ * Device memory is HIP device memory of the weight's device; streams are
+ * hipStream_t passed as void* (null = the null stream).  Forward calls are
+ * asynchronous in stream order.
+ */
+#ifndef ULLM_LINEAR_H
+#define ULLM_LINEAR_H
+
+#include "ullm/hip.h"
+
+/* Extension statuses.  8..12 keep the values of the reference's private
+ * evidence ABI (native/hip/src/evidence_abi.h:13-17); new codes start at 13. */
+#ifndef ULLM_STATUS_HIP_TIMEOUT
+#define ULLM_STATUS_HIP_TIMEOUT UINT32_C(8)
+#define ULLM_STATUS_HIP_INVALID_HANDLE UINT32_C(9)
+#define ULLM_STATUS_HIP_ZERO_DISPATCH UINT32_C(10)
+#define ULLM_STATUS_HIP_RUNTIME_ERROR UINT32_C(11)
+#define ULLM_STATUS_HIP_DISPATCH_CONTRACT UINT32_C(12)
+#endif
+#define ULLM_STATUS_OUT_OF_MEMORY UINT32_C(13)
+
+/* Weight encodings.  The reference's Encoding enum (crates/ullm-core/src/
+ * dtype.rs:55-66) has no variant for either; these are the values a future
+ * Encoding::Fp8RowScaled / Encoding::Aq4 would map to. */
+typedef uint32_t ullm_linear_encoding_t;
+/* u8 E4M3FN codes [N][K] + f32 scale per row [N]. */
+#define ULLM_LINEAR_ENCODING_FP8_E4M3_ROW UINT32_C(1)
+/* u32 words [N][K/8] (nibble j of word w is k = 8w + j, low nibble first)
+ * + f16 scale [N][K/128] + f16 zero [N][K/128]; K % 128 == 0. */
+#define ULLM_LINEAR_ENCODING_AQ4_G128 UINT32_C(2)
+
+/* What ullm_linear_weight_desc_t.values holds. */
+#define ULLM_LINEAR_SOURCE_F32 UINT32_C(1)     /* f32 [N][K], quantized here */
+#define ULLM_LINEAR_SOURCE_ENCODED UINT32_C(2) /* already-encoded buffers */
+
+/* Where caller buffers live. */
+#define ULLM_MEMORY_HOST UINT32_C(1)
+#define ULLM_MEMORY_DEVICE UINT32_C(2)
+
+/* Element types of activations and outputs (names as DType in
+ * crates/ullm-core/src/dtype.rs:6-16). */
+#define ULLM_LINEAR_DTYPE_BF16 UINT32_C(1)
+#define ULLM_LINEAR_DTYPE_F32 UINT32_C(2)
+#define ULLM_LINEAR_DTYPE_F8E4M3FN UINT32_C(3)
+
+/* How bf16 activations enter the contraction. */
+/* Exact: bf16 activations times dequantized weights, fp32 accumulation.
+ * Any M; the decode kernels serve M <= 32 per weight pass. */
+#define ULLM_LINEAR_ACT_EXACT UINT32_C(0)
+/* Prefill: activations are quantized per token to E4M3 (scale = max|x|/448)
+ * and contracted with FP8 weights on the FP8 matrix cores. */
+#define ULLM_LINEAR_ACT_FP8_PER_TOKEN UINT32_C(1)
+
+typedef struct ullm_linear_weight_t ullm_linear_weight_t;
+
+typedef struct ullm_linear_weight_desc_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint32_t encoding; /* ULLM_LINEAR_ENCODING_* */
+  uint32_t source;   /* ULLM_LINEAR_SOURCE_* */
+  uint64_t n;        /* output features, >= 1 */
+  uint64_t k;        /* input features, >= 1 (AQ4: multiple of 128) */
+  uint32_t memory;   /* ULLM_MEMORY_* of values/scales/zeros */
+  int32_t device;    /* HIP device ordinal that will own the weight */
+  const void *values;
+  const void *scales; /* ENCODED only */
+  const void *zeros;  /* ENCODED AQ4 only */
+  void *stream;       /* upload/quantize stream; creation blocks until done */
+  uint64_t reserved[4];
+} ullm_linear_weight_desc_t;
+
+typedef struct ullm_linear_weight_info_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint32_t encoding;
+  int32_t device;
+  uint64_t n;
+  uint64_t k;
+  uint64_t device_bytes; /* bytes the weight holds in HBM */
+  uint64_t reserved[4];
+} ullm_linear_weight_info_t;
+
+typedef struct ullm_linear_forward_desc_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  const ullm_linear_weight_t *weight;
+  uint64_t m;            /* rows of X and Y; 0 is a no-op */
+  const void *x;         /* device, x_dtype [M][x_row_stride] */
+  uint64_t x_row_stride; /* elements, 0 = K */
+  const float *x_scales; /* device f32 [M]; required iff x_dtype is E4M3 */
+  void *y;               /* device, y_dtype [M][y_row_stride] */
+  uint64_t y_row_stride; /* elements, 0 = N */
+  uint32_t x_dtype;      /* BF16, or F8E4M3FN (pre-quantized, FP8 weights) */
+  uint32_t y_dtype;      /* BF16 (RNE) or F32 */
+  uint32_t activation_mode; /* ULLM_LINEAR_ACT_*, for BF16 x */
+  float alpha;              /* output multiplier; 1.0f for a plain product */
+  void *stream;
+  void *workspace; /* device scratch for ACT_FP8_PER_TOKEN; null = library-owned */
+  uint64_t workspace_size;
+  uint64_t reserved[4];
+} ullm_linear_forward_desc_t;
+
+typedef struct ullm_linear_act_quant_desc_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint64_t m;
+  uint64_t k;
+  const void *x;         /* device bf16 [M][x_row_stride] */
+  uint64_t x_row_stride; /* elements, 0 = K */
+  void *xq;              /* device u8 E4M3FN [M][K] */
+  float *x_scales;       /* device f32 [M] */
+  void *stream;
+  uint64_t reserved[4];
+} ullm_linear_act_quant_desc_t;
+
+typedef struct ullm_linear_weight_export_desc_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint32_t memory; /* ULLM_MEMORY_* of the destination buffers */
+  uint32_t reserved0;
+  void *values; /* canonical layout of the weight's encoding */
+  void *scales;
+  void *zeros; /* AQ4 only */
+  void *stream;
+  uint64_t reserved[4];
+} ullm_linear_weight_export_desc_t;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Create a device-resident weight.  SOURCE_F32 quantizes on the GPU with the
+ * encoding's recipe; SOURCE_ENCODED uploads canonical encoded bytes.  Either
+ * way the weight is repacked into the device tile layout the kernels stream.
+ * Blocks until the weight is ready. */
+ULLM_HIP_API ullm_status_t ullm_linear_weight_create(
+    const ullm_linear_weight_desc_t *desc, ullm_linear_weight_t **weight,
+    ullm_error_sink_t *error_sink);
+
+/* Destroy and null *weight.  Waits for the device to finish using it. */
+ULLM_HIP_API ullm_status_t ullm_linear_weight_destroy(
+    ullm_linear_weight_t **weight, ullm_error_sink_t *error_sink);
+
+ULLM_HIP_API ullm_status_t ullm_linear_weight_query(
+    const ullm_linear_weight_t *weight, ullm_linear_weight_info_t *info,
+    ullm_error_sink_t *error_sink);
+
+/* Write the canonical encoded bytes back out (exact inverse of the repack). */
+ULLM_HIP_API ullm_status_t ullm_linear_weight_export(
+    const ullm_linear_weight_t *weight,
+    const ullm_linear_weight_export_desc_t *desc,
+    ullm_error_sink_t *error_sink);
+
+/* Parity/debug: dequantized weights as f32 [N][K] into device memory, with
+ * the exact operation order of the encoding's definition.  Stream-ordered. */
+ULLM_HIP_API ullm_status_t ullm_linear_weight_dequantize(
+    const ullm_linear_weight_t *weight, float *out, void *stream,
+    ullm_error_sink_t *error_sink);
+
+/* Y = alpha * X * W^T.  Stream-ordered. */
+ULLM_HIP_API ullm_status_t ullm_linear_forward(
+    const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink);
+
+/* Bytes of workspace ullm_linear_forward needs for this descriptor (0 for the
+ * exact path). */
+ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
+    const ullm_linear_forward_desc_t *desc, uint64_t *bytes,
+    ullm_error_sink_t *error_sink);
+
+/* Per-token E4M3 quantization of bf16 activations.  Stream-ordered. */
+ULLM_HIP_API ullm_status_t ullm_linear_quantize_activations(
+    const ullm_linear_act_quant_desc_t *desc, ullm_error_sink_t *error_sink);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* ULLM_LINEAR_H */

@@ -1,0 +1,163 @@
+"""GPU parity of the HIP linear path against the C oracle, through the C ABI.
+
+Bit-exact: weight quantization (FP8 rows, AQ4 g128), the canonical export of
+the device tile layout, dequantization, per-token activation quantization.
+Within 1e-2 x RMS of the fp32-accumulated oracle: the decode GEMV (FP8, AQ4)
+and the prefill FP8 GEMM.  Shapes cover the boundary policy of the reference
+(0/1/3/7, B-1/B/B+1 around the 16-row stripe, 64-k tile and 128-k group,
+17/37/73) at sizes the oracle finishes in seconds.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import (activations_bf16, assert_close, bf16_tensor_to_f32,
+                     to_torch_bf16, weights)
+
+pytestmark = pytest.mark.gpu
+
+FP8_SHAPES = [(1, 1), (3, 17), (15, 63), (16, 64), (17, 65), (37, 255),
+              (73, 513), (64, 4096)]
+AQ4_SHAPES = [(1, 128), (3, 256), (15, 384), (16, 128), (17, 640), (73, 1024),
+              (64, 4096)]
+
+
+def _fp8_weight(uh, w, dev):
+    return uh.LinearWeight.quantize(torch.from_numpy(w).to(dev),
+                                    uh.ENCODING_FP8_E4M3_ROW)
+
+
+def _aq4_weight(uh, w, dev):
+    return uh.LinearWeight.quantize(torch.from_numpy(w).to(dev),
+                                    uh.ENCODING_AQ4_G128)
+
+
+@pytest.mark.parametrize("n,k", FP8_SHAPES)
+def test_fp8_quantize_export_dequant_bit_exact(uh, orc, gpu, n, k):
+    w = weights(n, k, tag=n * 7 + k)
+    w[0, : min(k, 5)] = 0.0
+    if n > 2:
+        w[2, :] = 0.0  # all-zero row: s = 0, q = 0
+    q_ref, s_ref = orc.fp8_quantize_rows(w)
+    lw = _fp8_weight(uh, w, gpu)
+    q, s = lw.export()
+    assert np.array_equal(q, q_ref)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+    d = lw.dequantize().cpu().numpy()
+    d_ref = orc.fp8_dequantize(q_ref, s_ref)
+    assert np.array_equal(d.view(np.uint32), d_ref.view(np.uint32))
+    # upload of canonical bytes reproduces the same device weight
+    lw2 = uh.LinearWeight.from_fp8(q_ref, s_ref)
+    q2, s2 = lw2.export()
+    assert np.array_equal(q2, q_ref) and np.array_equal(s2, s_ref)
+
+
+@pytest.mark.parametrize("n,k", AQ4_SHAPES)
+def test_aq4_quantize_export_dequant_bit_exact(uh, orc, gpu, n, k):
+    w = weights(n, k, tag=n * 11 + k)
+    w[0, :128] = 0.25  # constant group: degenerate scale
+    if n > 1:
+        w[1, :128] = np.linspace(0.01, 0.05, 128)  # all-positive group
+    p_ref, s_ref, z_ref = orc.aq4_quantize(w)
+    lw = _aq4_weight(uh, w, gpu)
+    p, s, z = lw.export()
+    assert np.array_equal(s, s_ref)
+    assert np.array_equal(z, z_ref)
+    assert np.array_equal(p, p_ref)
+    d = lw.dequantize().cpu().numpy()
+    d_ref = orc.aq4_dequantize(p_ref, s_ref, z_ref)
+    assert np.array_equal(d.view(np.uint32), d_ref.view(np.uint32))
+    lw2 = uh.LinearWeight.from_aq4(p_ref, s_ref, z_ref)
+    p2, s2, z2 = lw2.export()
+    assert np.array_equal(p2, p_ref) and np.array_equal(s2, s_ref) \
+        and np.array_equal(z2, z_ref)
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 7, 16, 17, 32, 33, 70])
+@pytest.mark.parametrize("n,k", [(17, 65), (64, 4096), (129, 640), (16, 4096)])
+def test_fp8_gemv_parity(uh, orc, gpu, m, n, k):
+    w = weights(n, k, tag=3)
+    q, s = orc.fp8_quantize_rows(w)
+    xb = activations_bf16(orc, m, k, tag=m)
+    y_ref, _ = orc.fp8_gemv(xb, q, s)
+    lw = uh.LinearWeight.from_fp8(q, s)
+    x = to_torch_bf16(xb, gpu)
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what="fp8 gemv f32")
+    yb = lw.forward(x)
+    assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="fp8 gemv bf16")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 7, 16, 17, 32, 33])
+@pytest.mark.parametrize("n,k", [(17, 128), (64, 4096), (129, 640), (16, 1024)])
+def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
+    w = weights(n, k, tag=5)
+    p, s, z = orc.aq4_quantize(w)
+    xb = activations_bf16(orc, m, k, tag=m + 100)
+    y_ref, _ = orc.aq4_gemv(xb, p, s, z)
+    lw = uh.LinearWeight.from_aq4(p, s, z)
+    x = to_torch_bf16(xb, gpu)
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what="aq4 gemv f32")
+    yb = lw.forward(x)
+    assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="aq4 gemv bf16")
+
+
+def test_gemv_strided_activation_and_alpha(uh, orc, gpu):
+    n, k, m = 48, 384, 5
+    w = weights(n, k, tag=9)
+    q, s = orc.fp8_quantize_rows(w)
+    p, sz, z = orc.aq4_quantize(w)
+    wide = activations_bf16(orc, m, k + 40, tag=9)
+    xb = np.ascontiguousarray(wide[:, 8:8 + k])
+    big = to_torch_bf16(wide, gpu)
+    view = big[:, 8:8 + k]  # row stride k + 40, 16-byte aligned start
+    odd = big[:, 3:3 + k]  # unaligned start
+    for lw, ref in ((uh.LinearWeight.from_fp8(q, s), orc.fp8_gemv(xb, q, s, alpha=0.5)[0]),
+                    (uh.LinearWeight.from_aq4(p, sz, z), orc.aq4_gemv(xb, p, sz, z, alpha=0.5)[0])):
+        y = lw.forward(view, out_dtype=torch.float32, alpha=0.5)
+        assert_close(y.cpu().numpy(), ref, what="strided")
+    xo = np.ascontiguousarray(wide[:, 3:3 + k])
+    y = uh.LinearWeight.from_fp8(q, s).forward(odd, out_dtype=torch.float32)
+    assert_close(y.cpu().numpy(), orc.fp8_gemv(xo, q, s)[0], what="unaligned")
+
+
+@pytest.mark.parametrize("m,k", [(1, 1), (3, 17), (7, 255), (16, 4096), (33, 513)])
+def test_activation_quant_bit_exact(uh, orc, gpu, m, k):
+    xb = activations_bf16(orc, m, k, tag=k)
+    if m > 2:
+        xb[1, :] = 0  # all-zero token
+        xb[2, 0] = orc.bf16_from_f32(np.array([1e-30], np.float32))[0]
+    xq_ref, xs_ref = orc.act_quantize(xb)
+    xq, xs = uh.quantize_activations(to_torch_bf16(xb, gpu))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (7, 17, 65), (64, 64, 512),
+                                   (130, 100, 1000), (256, 256, 4096)])
+def test_fp8_gemm_parity(uh, orc, gpu, m, n, k):
+    w = weights(n, k, tag=13)
+    q, s = orc.fp8_quantize_rows(w)
+    xb = activations_bf16(orc, m, k, tag=14)
+    xq, xs = orc.act_quantize(xb)
+    y_ref, _ = orc.fp8_gemm(xq, xs, q, s)
+    lw = uh.LinearWeight.from_fp8(q, s)
+    x = to_torch_bf16(xb, gpu)
+    y = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN)
+    assert_close(y.cpu().numpy(), y_ref, what="fp8 gemm (quantize inside)")
+    # pre-quantized activations
+    xq_t = torch.from_numpy(xq).to(gpu)
+    xs_t = torch.from_numpy(xs).to(gpu)
+    y2 = lw.forward(xq_t, x_scales=xs_t)
+    assert_close(bf16_tensor_to_f32(y2), y_ref, bf16_out=True, what="fp8 gemm bf16")
+
+
+def test_zero_rows_is_noop(uh, orc, gpu):
+    q, s = orc.fp8_quantize_rows(weights(16, 64))
+    lw = uh.LinearWeight.from_fp8(q, s)
+    x = torch.empty((0, 64), dtype=torch.bfloat16, device=gpu)
+    y = lw.forward(x)
+    assert y.shape == (0, 16)

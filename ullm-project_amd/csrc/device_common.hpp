@@ -1,0 +1,143 @@
+// device_common.hpp -- gfx950 device helpers shared by the linear kernels.
+//
+// Number formats follow the definitions of the quantized linear path:
+// OCP E4M3FN (bias 7, max 448, NaN 0x7F, saturating RNE encode), bf16 RNE,
+// IEEE f16.  Every conversion here is exact or round-to-nearest-even and
+// must agree bit for bit with the CPU oracle used by the tests.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ullm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bit casts
+__device__ __forceinline__ uint32_t f32_bits(float x) {
+  return __builtin_bit_cast(uint32_t, x);
+}
+__device__ __forceinline__ float bits_f32(uint32_t b) {
+  return __builtin_bit_cast(float, b);
+}
+
+// bf16 <-> f32.  Decode is a shift; encode is round-to-nearest-even on the 16
+// dropped bits, with NaN kept quiet and overflow carrying into infinity.
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return bits_f32(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  const uint32_t b = f32_bits(x);
+  if ((b & 0x7fffffffu) > 0x7f800000u) {
+    return static_cast<uint16_t>((b >> 16) | 0x0040u);
+  }
+  return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// f16 <-> f32 through the hardware converts (RNE, f16 denormals preserved).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float x) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// E4M3FN decode from the format definition: exponent field 0 is subnormal
+// (m * 2^-9), otherwise (8 + m) * 2^(e - 10).  0x7F/0xFF are NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t code) {
+  const uint32_t mag = code & 0x7fu;
+  const uint32_t e = mag >> 3;
+  const uint32_t m = mag & 7u;
+  float v;
+  if (mag == 0x7fu) {
+    v = __builtin_nanf("");
+  } else if (e == 0) {
+    v = static_cast<float>(m) * 0.001953125f;  // 2^-9
+  } else {
+    // 2^(e-7) * (1 + m/8): rebias the exponent into f32 (127 - 7 = 120).
+    v = bits_f32(((e + 120u) << 23) | (m << 20));
+  }
+  return (code & 0x80u) ? -v : v;
+}
+
+// E4M3FN encode: RNE on the 20 dropped mantissa bits of an f32 in the normal
+// range, quantum 2^-9 below 2^-6, and saturation of |x| >= 448 to 448.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  const uint32_t b = f32_bits(x);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  const uint32_t a = b & 0x7fffffffu;
+  if (a > 0x7f800000u) {
+    return sign | 0x7fu;
+  }
+  if (a >= 0x43e00000u) {  // 448.0f
+    return sign | 0x7eu;
+  }
+  if (a < 0x3c800000u) {  // 2^-6: multiples of 2^-9, 8 * 2^-9 is code 0x08
+    const float v = bits_f32(a) * 512.0f;
+    return sign | static_cast<uint32_t>(__builtin_rintf(v));
+  }
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return sign | ((r >> 20) - (120u << 3));
+}
+
+// ------------------------------------------------------------ MFMA helpers
+// v_mfma_f32_16x16x32_bf16: src0 lane l carries row (l % 16), k-slots
+// 8*(l/16)..+7; src1 lane l carries column (l % 16) for the same k-slots;
+// the result lane l holds rows 4*(l/16)+r, column l % 16, r = 0..3.
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Four E4M3 codes in one dword -> four bf16 (exact: every E4M3 value is a
+// bf16 value).  Scale 1.0 makes the scaled convert a plain convert.
+__device__ __forceinline__ u32x2 e4m3x4_to_bf16x4(uint32_t w) {
+  const bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  const bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  u32x2 r;
+  r.x = __builtin_bit_cast(uint32_t, lo);
+  r.y = __builtin_bit_cast(uint32_t, hi);
+  return r;
+}
+
+// Eight 4-bit codes in one dword -> eight bf16 holding 128 + q, exact because
+// 128..143 need 8 significant bits.  Element t of the result is nibble
+// (t / 2) + 4 * (t % 2) of w: OR-ing a nibble into the low mantissa bits of
+// bf16 128.0 (0x4300) yields 128 + q.
+__device__ __forceinline__ bf16x8 nib8_to_bf16_off128(uint32_t w) {
+  u32x4 r;
+  r.x = (w & 0x000f000fu) | 0x43004300u;
+  r.y = ((w >> 4) & 0x000f000fu) | 0x43004300u;
+  r.z = ((w >> 8) & 0x000f000fu) | 0x43004300u;
+  r.w = ((w >> 12) & 0x000f000fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Nibble position inside a device AQ4 word for MFMA element t (inverse of the
+// mapping in nib8_to_bf16_off128).
+__host__ __device__ constexpr uint32_t aq4_nibble_pos(uint32_t t) {
+  return (t >> 1) + 4u * (t & 1u);
+}
+
+// ------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    v = fmaxf(v, __shfl_xor(v, off, kWave));
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    v = fminf(v, __shfl_xor(v, off, kWave));
+  }
+  return v;
+}
+
+}  // namespace ullm

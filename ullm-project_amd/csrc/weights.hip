@@ -1,0 +1,316 @@
+// weights.hip -- quantization, repacking, export and dequantization of
+// device-resident weights, and per-token activation quantization.
+//
+// These kernels run once per weight (creation) or are parity/debug tools; the
+// activation quantizer is on the prefill path and is HBM-bound (2 bytes read,
+// 1 byte written per element).  All arithmetic that defines a quantized value
+// is written with FMA contraction off so it matches the format definitions
+// bit for bit: q = enc(w / s), dequant = dec(q) * s, AQ4 dequant = (q - z) * s.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ullm {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ float block_max(float v, float *red) {
+  v = wave_max(v);
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    red[wave] = v;
+  }
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < kBlock / kWave; ++i) {
+    r = fmaxf(r, red[i]);
+  }
+  return r;
+}
+
+// --------------------------------------------------------------- FP8 rows
+// One workgroup per weight row: s = max|w| / 448, q = e4m3(w / s).
+__global__ __launch_bounds__(kBlock) void fp8_quantize_kernel(
+    const float *__restrict__ w, Fp8Layout L, uint8_t *__restrict__ tiles,
+    float *__restrict__ scales) {
+  __shared__ float red[kBlock / kWave];
+  const uint64_t row = blockIdx.x;
+  const float *src = w + row * L.k;
+  float amax = 0.0f;
+  for (uint64_t c = threadIdx.x; c < L.k; c += kBlock) {
+    amax = fmaxf(amax, fabsf(src[c]));
+  }
+  amax = block_max(amax, red);
+  const float s = amax / 448.0f;
+  if (threadIdx.x == 0) {
+    scales[row] = s;
+  }
+  for (uint64_t c = threadIdx.x; c < L.k; c += kBlock) {
+    const uint32_t q = s == 0.0f ? 0u : f32_to_e4m3(src[c] / s);
+    tiles[L.offset(row, c)] = static_cast<uint8_t>(q);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void fp8_pack_kernel(
+    const uint8_t *__restrict__ q, const float *__restrict__ s_in, Fp8Layout L,
+    uint8_t *__restrict__ tiles, float *__restrict__ scales) {
+  const uint64_t total = L.n * L.k;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / L.k, col = i % L.k;
+    tiles[L.offset(row, col)] = q[i];
+    if (col == 0) {
+      scales[row] = s_in[row];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void fp8_export_kernel(
+    const uint8_t *__restrict__ tiles, const float *__restrict__ scales,
+    Fp8Layout L, uint8_t *__restrict__ q, float *__restrict__ s_out) {
+  const uint64_t total = L.n * L.k;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / L.k, col = i % L.k;
+    q[i] = tiles[L.offset(row, col)];
+    if (col == 0) {
+      s_out[row] = scales[row];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void fp8_dequant_kernel(
+    const uint8_t *__restrict__ tiles, const float *__restrict__ scales,
+    Fp8Layout L, float *__restrict__ out) {
+  const uint64_t total = L.n * L.k;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / L.k, col = i % L.k;
+    out[i] = e4m3_to_f32(tiles[L.offset(row, col)]) * scales[row];
+  }
+}
+
+// ---------------------------------------------------------------- AQ4 g128
+__device__ __forceinline__ uint64_t aq4_word(const Aq4Layout &L, uint64_t row,
+                                             uint64_t g, uint32_t q4,
+                                             uint32_t j) {
+  return (((row / 16) * L.groups + g) * 64 + (row % 16) + 16 * q4) * 4 + j;
+}
+__device__ __forceinline__ uint64_t aq4_sz(const Aq4Layout &L, uint64_t row,
+                                           uint64_t g) {
+  return ((row / 16) * L.groups + g) * 16 + row % 16;
+}
+
+// One wavefront per (row, group of 128).
+__global__ __launch_bounds__(kWave) void aq4_quantize_kernel(
+    const float *__restrict__ w, Aq4Layout L, uint32_t *__restrict__ tiles,
+    uint32_t *__restrict__ sz) {
+  __shared__ uint8_t codes[128];
+  const uint64_t g = blockIdx.x;
+  const uint64_t row = blockIdx.y;
+  const uint32_t lane = threadIdx.x;
+  const float *src = w + row * L.k + g * 128;
+  const float v0 = src[lane];
+  const float v1 = src[lane + 64];
+  const float lo = wave_min(fminf(v0, v1));
+  const float hi = wave_max(fmaxf(v0, v1));
+  uint16_t s16 = f32_to_f16((hi - lo) / 15.0f);
+  float sf = f16_to_f32(s16);
+  uint16_t z16 = sf != 0.0f ? f32_to_f16(-lo / sf) : uint16_t(0);
+  if (sf == 0.0f || !__builtin_isfinite(f16_to_f32(z16))) {
+    s16 = 0x3c00u;  // 1.0
+    z16 = f32_to_f16(-lo);
+    sf = 1.0f;
+  }
+  const float zf = f16_to_f32(z16);
+  const float u0 = __builtin_rintf(v0 / sf + zf);
+  const float u1 = __builtin_rintf(v1 / sf + zf);
+  codes[lane] = static_cast<uint8_t>(fminf(fmaxf(u0, 0.0f), 15.0f));
+  codes[lane + 64] = static_cast<uint8_t>(fminf(fmaxf(u1, 0.0f), 15.0f));
+  __syncthreads();
+  if (lane < 16) {
+    const uint32_t q4 = lane / 4, j = lane % 4;
+    uint32_t word = 0;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t) {
+      word |= uint32_t(codes[32 * j + 8 * q4 + t]) << (4 * aq4_nibble_pos(t));
+    }
+    tiles[aq4_word(L, row, g, q4, j)] = word;
+  }
+  if (lane == 0) {
+    sz[aq4_sz(L, row, g)] = uint32_t(s16) | (uint32_t(z16) << 16);
+  }
+}
+
+// One thread per canonical dword (row, w): the 8 codes k = 8w .. 8w+7 form
+// exactly one device dword, with nibbles permuted to MFMA element order.
+__global__ __launch_bounds__(kBlock) void aq4_pack_kernel(
+    const uint32_t *__restrict__ packed, const uint16_t *__restrict__ scales,
+    const uint16_t *__restrict__ zeros, Aq4Layout L,
+    uint32_t *__restrict__ tiles, uint32_t *__restrict__ sz) {
+  const uint64_t wpr = L.k / 8;
+  const uint64_t total = L.n * wpr;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / wpr, w = i % wpr;
+    const uint64_t g = w / 16;
+    const uint32_t j = (w % 16) / 4, q4 = w % 4;
+    const uint32_t src = packed[i];
+    uint32_t word = 0;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t) {
+      word |= ((src >> (4 * t)) & 0xfu) << (4 * aq4_nibble_pos(t));
+    }
+    tiles[aq4_word(L, row, g, q4, j)] = word;
+    if (w % 16 == 0) {
+      const uint64_t si = row * L.groups + g;
+      sz[aq4_sz(L, row, g)] = uint32_t(scales[si]) | (uint32_t(zeros[si]) << 16);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void aq4_export_kernel(
+    const uint32_t *__restrict__ tiles, const uint32_t *__restrict__ sz,
+    Aq4Layout L, uint32_t *__restrict__ packed, uint16_t *__restrict__ scales,
+    uint16_t *__restrict__ zeros) {
+  const uint64_t wpr = L.k / 8;
+  const uint64_t total = L.n * wpr;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / wpr, w = i % wpr;
+    const uint64_t g = w / 16;
+    const uint32_t j = (w % 16) / 4, q4 = w % 4;
+    const uint32_t dev = tiles[aq4_word(L, row, g, q4, j)];
+    uint32_t word = 0;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t) {
+      word |= ((dev >> (4 * aq4_nibble_pos(t))) & 0xfu) << (4 * t);
+    }
+    packed[i] = word;
+    if (w % 16 == 0) {
+      const uint32_t v = sz[aq4_sz(L, row, g)];
+      scales[row * L.groups + g] = uint16_t(v & 0xffffu);
+      zeros[row * L.groups + g] = uint16_t(v >> 16);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void aq4_dequant_kernel(
+    const uint32_t *__restrict__ tiles, const uint32_t *__restrict__ sz,
+    Aq4Layout L, float *__restrict__ out) {
+  const uint64_t total = L.n * L.k;
+  for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
+       i += uint64_t(gridDim.x) * kBlock) {
+    const uint64_t row = i / L.k, col = i % L.k;
+    const uint64_t g = col / 128;
+    const uint32_t kk = col % 128;
+    const uint32_t j = kk / 32, q4 = (kk % 32) / 8, t = kk % 8;
+    const uint32_t dev = tiles[aq4_word(L, row, g, q4, j)];
+    const uint32_t code = (dev >> (4 * aq4_nibble_pos(t))) & 0xfu;
+    const uint32_t v = sz[aq4_sz(L, row, g)];
+    const float sf = f16_to_f32(uint16_t(v & 0xffffu));
+    const float zf = f16_to_f32(uint16_t(v >> 16));
+    out[i] = (float(code) - zf) * sf;
+  }
+}
+
+// ------------------------------------------------------ activation quant
+// One workgroup per token row: a = max|x| / 448, xq = e4m3(x / a).
+__global__ __launch_bounds__(kBlock) void act_quant_kernel(
+    const uint16_t *__restrict__ x, uint64_t ldx, uint64_t k,
+    uint8_t *__restrict__ xq, float *__restrict__ xs) {
+  __shared__ float red[kBlock / kWave];
+  const uint64_t row = blockIdx.x;
+  const uint16_t *src = x + row * ldx;
+  float amax = 0.0f;
+  for (uint64_t c = threadIdx.x; c < k; c += kBlock) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(src[c])));
+  }
+  amax = block_max(amax, red);
+  const float a = amax / 448.0f;
+  if (threadIdx.x == 0) {
+    xs[row] = a;
+  }
+  for (uint64_t c = threadIdx.x; c < k; c += kBlock) {
+    const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(src[c]) / a);
+    xq[row * k + c] = static_cast<uint8_t>(q);
+  }
+}
+
+unsigned grid_for(uint64_t total) {
+  const uint64_t blocks = (total + kBlock - 1) / kBlock;
+  return static_cast<unsigned>(blocks < 65536 ? (blocks ? blocks : 1) : 65536);
+}
+
+}  // namespace
+
+hipError_t launch_fp8_quantize(const float *w, const Fp8Layout &L,
+                               uint8_t *tiles, float *scales, hipStream_t s) {
+  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(L.n), dim3(kBlock), 0, s, w, L,
+                     tiles, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_pack(const uint8_t *q, const float *scales_in,
+                           const Fp8Layout &L, uint8_t *tiles, float *scales,
+                           hipStream_t s) {
+  hipLaunchKernelGGL(fp8_pack_kernel, dim3(grid_for(L.n * L.k)), dim3(kBlock),
+                     0, s, q, scales_in, L, tiles, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_export(const uint8_t *tiles, const float *scales,
+                             const Fp8Layout &L, uint8_t *q, float *s_out,
+                             hipStream_t s) {
+  hipLaunchKernelGGL(fp8_export_kernel, dim3(grid_for(L.n * L.k)),
+                     dim3(kBlock), 0, s, tiles, scales, L, q, s_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_dequant(const uint8_t *tiles, const float *scales,
+                              const Fp8Layout &L, float *out, hipStream_t s) {
+  hipLaunchKernelGGL(fp8_dequant_kernel, dim3(grid_for(L.n * L.k)),
+                     dim3(kBlock), 0, s, tiles, scales, L, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_aq4_quantize(const float *w, const Aq4Layout &L,
+                               uint32_t *tiles, uint32_t *sz, hipStream_t s) {
+  hipLaunchKernelGGL(aq4_quantize_kernel, dim3(L.groups, L.n), dim3(kWave), 0,
+                     s, w, L, tiles, sz);
+  return hipGetLastError();
+}
+
+hipError_t launch_aq4_pack(const uint32_t *packed, const uint16_t *scales,
+                           const uint16_t *zeros, const Aq4Layout &L,
+                           uint32_t *tiles, uint32_t *sz, hipStream_t s) {
+  hipLaunchKernelGGL(aq4_pack_kernel, dim3(grid_for(L.n * (L.k / 8))),
+                     dim3(kBlock), 0, s, packed, scales, zeros, L, tiles, sz);
+  return hipGetLastError();
+}
+
+hipError_t launch_aq4_export(const uint32_t *tiles, const uint32_t *sz,
+                             const Aq4Layout &L, uint32_t *packed,
+                             uint16_t *scales, uint16_t *zeros, hipStream_t s) {
+  hipLaunchKernelGGL(aq4_export_kernel, dim3(grid_for(L.n * (L.k / 8))),
+                     dim3(kBlock), 0, s, tiles, sz, L, packed, scales, zeros);
+  return hipGetLastError();
+}
+
+hipError_t launch_aq4_dequant(const uint32_t *tiles, const uint32_t *sz,
+                              const Aq4Layout &L, float *out, hipStream_t s) {
+  hipLaunchKernelGGL(aq4_dequant_kernel, dim3(grid_for(L.n * L.k)),
+                     dim3(kBlock), 0, s, tiles, sz, L, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_quant(const uint16_t *x, uint64_t ldx, uint64_t m,
+                            uint64_t k, uint8_t *xq, float *xs, hipStream_t s) {
+  hipLaunchKernelGGL(act_quant_kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k,
+                     xq, xs);
+  return hipGetLastError();
+}
+
+}  // namespace ullm

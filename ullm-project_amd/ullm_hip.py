@@ -1,0 +1,403 @@
+"""Python host mirror of the uLLM HIP backend over its C ABI.
+
+Mirrors the reference's Rust layering:
+  * the ``ullm_*`` ctypes declarations play the part of ``ullm-hip-sys``
+    (reference crates/ullm-hip-sys/src/bindings.rs:1-119);
+  * ``Status``, ``HipError``, ``abi_version``, ``version``, ``backend_probe``,
+    ``context_probe`` mirror ``ullm-hip`` (reference
+    crates/ullm-hip/src/lib.rs:20-76 Status, :78-113 HipError, :189-268
+    probes) with the same 256-byte diagnostic buffers (lib.rs:18,154-170);
+  * ``LinearWeight`` / ``linear_forward`` / ``quantize_activations`` wrap the
+    linear-layer extension of include/ullm/linear.h, the calls a future
+    ``HipBackend::execute`` (reference crates/ullm-hip/src/lib.rs:487-513)
+    would make for a Matmul with a quantized weight.
+
+PyTorch is used only to hold device memory and to name streams.  There is no
+fallback: if the native library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libullm_hip.so"
+ERROR_CAPACITY = 256
+ABI_VERSION = 1
+
+# ------------------------------------------------------------------ statuses
+
+
+class Status(enum.IntEnum):
+    OK = 0
+    INVALID_ARGUMENT = 1
+    BUFFER_TOO_SMALL = 2
+    UNSUPPORTED = 3
+    HIP_UNAVAILABLE = 4
+    INVALID_ABI_VERSION = 5
+    RESERVED_NONZERO = 6
+    INTERNAL_ERROR = 7
+    HIP_TIMEOUT = 8
+    HIP_INVALID_HANDLE = 9
+    HIP_ZERO_DISPATCH = 10
+    HIP_RUNTIME_ERROR = 11
+    HIP_DISPATCH_CONTRACT = 12
+    OUT_OF_MEMORY = 13
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        try:
+            self.status = Status(status)
+        except ValueError:
+            self.status = status
+        self.message = message
+        super().__init__(f"{getattr(self.status, 'name', status)}: {message}")
+
+
+ENCODING_FP8_E4M3_ROW = 1
+ENCODING_AQ4_G128 = 2
+SOURCE_F32 = 1
+SOURCE_ENCODED = 2
+MEMORY_HOST = 1
+MEMORY_DEVICE = 2
+DTYPE_BF16 = 1
+DTYPE_F32 = 2
+DTYPE_F8E4M3FN = 3
+ACT_EXACT = 0
+ACT_FP8_PER_TOKEN = 1
+BACKEND_HIP = 1
+
+# ------------------------------------------------------------------- structs
+_u32 = ctypes.c_uint32
+_i32 = ctypes.c_int32
+_u64 = ctypes.c_uint64
+_vp = ctypes.c_void_p
+
+
+class ErrorSink(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("message", ctypes.c_char_p), ("message_capacity", _u64),
+                ("message_length", _u64), ("reserved", _u64 * 2)]
+
+
+class VersionInfo(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("major", _u32),
+                ("minor", _u32), ("patch", _u32), ("reserved", _u32 * 3)]
+
+
+class BackendProbeResult(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("backend", _u32),
+                ("available", _u32), ("hip_runtime_present", _u32),
+                ("reserved", _u32 * 3)]
+
+
+class ContextProbeResult(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("context_present", _u32), ("hip_available", _u32),
+                ("reserved", _u32 * 4)]
+
+
+class WeightDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("encoding", _u32), ("source", _u32), ("n", _u64), ("k", _u64),
+                ("memory", _u32), ("device", _i32), ("values", _vp),
+                ("scales", _vp), ("zeros", _vp), ("stream", _vp),
+                ("reserved", _u64 * 4)]
+
+
+class WeightInfo(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("encoding", _u32), ("device", _i32), ("n", _u64), ("k", _u64),
+                ("device_bytes", _u64), ("reserved", _u64 * 4)]
+
+
+class ForwardDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("weight", _vp),
+                ("m", _u64), ("x", _vp), ("x_row_stride", _u64),
+                ("x_scales", _vp), ("y", _vp), ("y_row_stride", _u64),
+                ("x_dtype", _u32), ("y_dtype", _u32), ("activation_mode", _u32),
+                ("alpha", ctypes.c_float), ("stream", _vp), ("workspace", _vp),
+                ("workspace_size", _u64), ("reserved", _u64 * 4)]
+
+
+class ActQuantDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("m", _u64),
+                ("k", _u64), ("x", _vp), ("x_row_stride", _u64), ("xq", _vp),
+                ("x_scales", _vp), ("stream", _vp), ("reserved", _u64 * 4)]
+
+
+class ExportDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("memory", _u32),
+                ("reserved0", _u32), ("values", _vp), ("scales", _vp),
+                ("zeros", _vp), ("stream", _vp), ("reserved", _u64 * 4)]
+
+
+def new(struct_type, **fields):
+    """A struct with its {struct_size, abi_version} header filled in."""
+    s = struct_type()
+    s.struct_size = ctypes.sizeof(struct_type)
+    s.abi_version = ABI_VERSION
+    for k, v in fields.items():
+        setattr(s, k, v)
+    return s
+
+
+# --------------------------------------------------------------- the library
+_SIGNATURES = {
+    "ullm_get_abi_version": [ctypes.POINTER(_u32), ctypes.POINTER(ErrorSink)],
+    "ullm_query_version": [ctypes.POINTER(VersionInfo), ctypes.POINTER(ErrorSink)],
+    "ullm_backend_probe": [_u32, ctypes.POINTER(BackendProbeResult),
+                           ctypes.POINTER(ErrorSink)],
+    "ullm_context_probe": [_vp, ctypes.POINTER(ContextProbeResult),
+                           ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_create": [ctypes.POINTER(WeightDesc), ctypes.POINTER(_vp),
+                                  ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_destroy": [ctypes.POINTER(_vp), ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_query": [_vp, ctypes.POINTER(WeightInfo),
+                                 ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_export": [_vp, ctypes.POINTER(ExportDesc),
+                                  ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_dequantize": [_vp, _vp, _vp, ctypes.POINTER(ErrorSink)],
+    "ullm_linear_forward": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(ErrorSink)],
+    "ullm_linear_workspace_size": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(_u64),
+                                   ctypes.POINTER(ErrorSink)],
+    "ullm_linear_quantize_activations": [ctypes.POINTER(ActQuantDesc),
+                                         ctypes.POINTER(ErrorSink)],
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libullm_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with ullm-project_amd/build.py")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, args in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _u32
+        _lib = L
+    return _lib
+
+
+class _Sink:
+    def __init__(self, capacity: int = ERROR_CAPACITY):
+        self.buf = ctypes.create_string_buffer(capacity)
+        self.sink = new(ErrorSink, message=ctypes.cast(self.buf, ctypes.c_char_p),
+                        message_capacity=capacity)
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.sink)
+
+    def text(self) -> str:
+        n = min(self.sink.message_length, len(self.buf) - 1)
+        return self.buf.raw[:n].decode(errors="replace")
+
+
+def _check(status: int, sink: _Sink):
+    if status != Status.OK:
+        raise HipError(status, sink.text())
+
+
+# ------------------------------------------------------------- v1 functions
+
+def abi_version() -> int:
+    s = _Sink()
+    v = _u32()
+    _check(lib().ullm_get_abi_version(ctypes.byref(v), s.ref), s)
+    return v.value
+
+
+def version() -> tuple:
+    s = _Sink()
+    info = new(VersionInfo)
+    _check(lib().ullm_query_version(ctypes.byref(info), s.ref), s)
+    return (info.major, info.minor, info.patch)
+
+
+def backend_probe():
+    """(available, hip_runtime_present, diagnostic) like ullm_hip::backend_probe."""
+    s = _Sink()
+    r = new(BackendProbeResult)
+    st = lib().ullm_backend_probe(BACKEND_HIP, ctypes.byref(r), s.ref)
+    if st not in (Status.OK, Status.HIP_UNAVAILABLE):
+        raise HipError(st, s.text())
+    return bool(r.available), bool(r.hip_runtime_present), s.text()
+
+
+def context_probe():
+    s = _Sink()
+    r = new(ContextProbeResult)
+    st = lib().ullm_context_probe(None, ctypes.byref(r), s.ref)
+    if st not in (Status.OK, Status.HIP_UNAVAILABLE):
+        raise HipError(st, s.text())
+    return bool(r.context_present), bool(r.hip_available), s.text()
+
+
+# ------------------------------------------------------------ linear layer
+
+def _ptr(t) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(stream, "cuda_stream", stream)
+
+
+class LinearWeight:
+    """A device-resident quantized weight W[N][K] (opaque native handle)."""
+
+    def __init__(self, handle: int, encoding: int, n: int, k: int, device: int):
+        self.handle = handle
+        self.encoding = encoding
+        self.n = n
+        self.k = k
+        self.device = device
+
+    # -- construction -----------------------------------------------------
+    @classmethod
+    def _create(cls, encoding, source, n, k, memory, device, values, scales=None,
+                zeros=None, stream=None):
+        s = _Sink()
+        d = new(WeightDesc, encoding=encoding, source=source, n=n, k=k,
+                memory=memory, device=device, values=values, scales=scales,
+                zeros=zeros, stream=stream)
+        h = _vp()
+        _check(lib().ullm_linear_weight_create(ctypes.byref(d), ctypes.byref(h),
+                                               s.ref), s)
+        return cls(h.value, encoding, n, k, device)
+
+    @classmethod
+    def quantize(cls, w, encoding: int, stream=None):
+        """Quantize an f32 weight tensor [N][K] (CUDA or CPU) on the GPU."""
+        import torch
+        assert w.dtype == torch.float32 and w.dim() == 2
+        w = w.contiguous()
+        n, k = w.shape
+        if w.is_cuda:
+            return cls._create(encoding, SOURCE_F32, n, k, MEMORY_DEVICE,
+                               w.device.index, _ptr(w), stream=_stream(stream))
+        return cls._create(encoding, SOURCE_F32, n, k, MEMORY_HOST, 0, _ptr(w),
+                           stream=None)
+
+    @classmethod
+    def from_fp8(cls, q, s, device=0, stream=None):
+        """Upload canonical E4M3 codes q uint8 [N][K] and f32 scales [N]."""
+        n, k = q.shape
+        mem = MEMORY_DEVICE if getattr(q, "is_cuda", False) else MEMORY_HOST
+        return cls._create(ENCODING_FP8_E4M3_ROW, SOURCE_ENCODED, n, k, mem,
+                           device, _addr(q), _addr(s), None,
+                           _stream(stream) if mem == MEMORY_DEVICE else None)
+
+    @classmethod
+    def from_aq4(cls, packed, scales, zeros, device=0, stream=None):
+        """Upload canonical AQ4: u32 [N][K/8], f16 bits [N][K/128] x 2."""
+        n = packed.shape[0]
+        k = packed.shape[1] * 8
+        mem = MEMORY_DEVICE if getattr(packed, "is_cuda", False) else MEMORY_HOST
+        return cls._create(ENCODING_AQ4_G128, SOURCE_ENCODED, n, k, mem, device,
+                           _addr(packed), _addr(scales), _addr(zeros),
+                           _stream(stream) if mem == MEMORY_DEVICE else None)
+
+    # -- lifetime ----------------------------------------------------------
+    def destroy(self):
+        if self.handle:
+            s = _Sink()
+            h = _vp(self.handle)
+            self.handle = None
+            _check(lib().ullm_linear_weight_destroy(ctypes.byref(h), s.ref), s)
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    def info(self) -> WeightInfo:
+        s = _Sink()
+        i = new(WeightInfo)
+        _check(lib().ullm_linear_weight_query(self.handle, ctypes.byref(i), s.ref), s)
+        return i
+
+    # -- debug / parity ----------------------------------------------------
+    def export(self):
+        """Canonical encoded buffers as numpy arrays (host)."""
+        import numpy as np
+        n, k = self.n, self.k
+        if self.encoding == ENCODING_FP8_E4M3_ROW:
+            v = np.empty((n, k), np.uint8)
+            sc = np.empty(n, np.float32)
+            z = None
+        else:
+            v = np.empty((n, k // 8), np.uint32)
+            sc = np.empty((n, k // 128), np.uint16)
+            z = np.empty((n, k // 128), np.uint16)
+        s = _Sink()
+        d = new(ExportDesc, memory=MEMORY_HOST, values=v.ctypes.data,
+                scales=sc.ctypes.data, zeros=None if z is None else z.ctypes.data)
+        _check(lib().ullm_linear_weight_export(self.handle, ctypes.byref(d), s.ref), s)
+        return (v, sc) if z is None else (v, sc, z)
+
+    def dequantize(self, stream=None):
+        import torch
+        out = torch.empty((self.n, self.k), dtype=torch.float32,
+                          device=f"cuda:{self.device}")
+        s = _Sink()
+        _check(lib().ullm_linear_weight_dequantize(self.handle, _ptr(out),
+                                                   _stream(stream), s.ref), s)
+        return out
+
+    # -- compute -----------------------------------------------------------
+    def forward(self, x, y=None, *, x_scales=None, out_dtype=None, alpha=1.0,
+                mode=ACT_EXACT, stream=None, workspace=None):
+        """y = alpha * x @ W^T for x bf16 [M][>=K] (row stride honoured) or
+        pre-quantized e4m3 (uint8) with x_scales."""
+        import torch
+        m = x.shape[0]
+        if y is None:
+            dt = out_dtype or torch.bfloat16
+            y = torch.empty((m, self.n), dtype=dt, device=x.device)
+        x_dtype = DTYPE_F8E4M3FN if x.dtype in (torch.uint8, torch.float8_e4m3fn) \
+            else DTYPE_BF16
+        d = new(ForwardDesc, weight=self.handle, m=m, x=_ptr(x),
+                x_row_stride=x.stride(0) if x.dim() == 2 else 0,
+                x_scales=_ptr(x_scales), y=_ptr(y), y_row_stride=y.stride(0),
+                x_dtype=x_dtype,
+                y_dtype=DTYPE_F32 if y.dtype == torch.float32 else DTYPE_BF16,
+                activation_mode=mode, alpha=alpha, stream=_stream(stream),
+                workspace=_ptr(workspace),
+                workspace_size=0 if workspace is None else workspace.numel() * workspace.element_size())
+        s = _Sink()
+        _check(lib().ullm_linear_forward(ctypes.byref(d), s.ref), s)
+        return y
+
+
+def _addr(a):
+    if a is None:
+        return None
+    if hasattr(a, "data_ptr"):
+        return int(a.data_ptr())
+    return int(a.ctypes.data)
+
+
+def quantize_activations(x, stream=None):
+    """Per-token E4M3 quantization: returns (xq uint8 [M][K], scales f32 [M])."""
+    import torch
+    m, k = x.shape
+    xq = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    xs = torch.empty((m,), dtype=torch.float32, device=x.device)
+    d = new(ActQuantDesc, m=m, k=k, x=_ptr(x), x_row_stride=x.stride(0),
+            xq=_ptr(xq), x_scales=_ptr(xs), stream=_stream(stream))
+    s = _Sink()
+    _check(lib().ullm_linear_quantize_activations(ctypes.byref(d), s.ref), s)
+    return xq, xs
