@@ -107,15 +107,29 @@ __device__ __forceinline__ u32x2 e4m3x4_to_bf16x4(uint32_t w) {
 
 // Eight 4-bit codes in one dword -> eight bf16 holding 128 + q, exact because
 // 128..143 need 8 significant bits.  Element t of the result is nibble
-// (t / 2) + 4 * (t % 2) of w: OR-ing a nibble into the low mantissa bits of
-// bf16 128.0 (0x4300) yields 128 + q.
-__device__ __forceinline__ bf16x8 nib8_to_bf16_off128(uint32_t w) {
+// (t / 2) + 4 * (t % 2) of w: inserting a nibble into the low mantissa bits
+// of bf16 128.0 (0x4300) yields 128 + q.  `mask` (0x000f000f) and `magic`
+// (0x43004300) come from opaque_u32() so they live in registers and each
+// insert compiles to one v_bfi_b32 (gfx9 VOP3 takes no literal operands).
+__device__ __forceinline__ bf16x8 nib8_to_bf16_off128(uint32_t w,
+                                                      uint32_t mask,
+                                                      uint32_t magic) {
   u32x4 r;
-  r.x = (w & 0x000f000fu) | 0x43004300u;
-  r.y = ((w >> 4) & 0x000f000fu) | 0x43004300u;
-  r.z = ((w >> 8) & 0x000f000fu) | 0x43004300u;
-  r.w = ((w >> 12) & 0x000f000fu) | 0x43004300u;
+  r.x = (w & mask) | (magic & ~mask);
+  r.y = ((w >> 4) & mask) | (magic & ~mask);
+  r.z = ((w >> 8) & mask) | (magic & ~mask);
+  r.w = ((w >> 12) & mask) | (magic & ~mask);
   return __builtin_bit_cast(bf16x8, r);
+}
+
+// A constant the compiler cannot fold into instructions (kept in a VGPR).
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 nib8_to_bf16_off128(uint32_t w) {
+  return nib8_to_bf16_off128(w, 0x000f000fu, 0x43004300u);
 }
 
 // Nibble position inside a device AQ4 word for MFMA element t (inverse of the

@@ -20,42 +20,57 @@
 // sum_k x) per group: the integer codes stay exact in bf16, the group sum of x
 // comes from a second MFMA against a ones operand, and the per-group scale and
 // zero are applied once per 128 k in fp32.
+#include <cstdlib>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
 namespace ullm {
 namespace {
 
-constexpr int kBatch = 8;  // tiles in flight per wave
-
-// Eight (or sixteen) bf16 of activation row m starting at k0.  Rows beyond M
-// and columns beyond K read as zero; `vec` says x rows are 16-byte aligned.
-__device__ __forceinline__ bf16x8 load_x8(const uint16_t *__restrict__ xrow,
-                                          bool valid, uint32_t k0, uint32_t K,
-                                          bool vec) {
-  u32x4 r = {0u, 0u, 0u, 0u};
-  if (valid) {
-    if (vec && k0 + 8 <= K) {
-      r = *reinterpret_cast<const u32x4 *>(xrow + k0);
+// Activation row reader.  VEC: rows are 16-byte aligned and K covers every
+// unit, so each read is one unconditional 16-byte load; lanes whose row is past
+// M read row 0 and zero the value with a select, keeping the code free of
+// branches (a branch around a load forces the wait counter to drain).  The
+// scalar variant handles unaligned views and ragged K.
+template <bool VEC>
+struct XRow {
+  const uint16_t *row;
+  bool valid;
+  uint32_t K;
+  XRow() = default;
+  __device__ __forceinline__ XRow(const uint16_t *x, uint64_t ldx, uint32_t m,
+                                  uint32_t M, uint32_t k)
+      : row(x + uint64_t(m < M ? m : 0) * ldx), valid(m < M), K(k) {}
+  __device__ __forceinline__ bf16x8 load8(uint32_t k0) const {
+    u32x4 r;
+    if constexpr (VEC) {
+      r = *reinterpret_cast<const u32x4 *>(row + k0);
+      const uint32_t keep = valid ? 0xffffffffu : 0u;
+      r.x &= keep;
+      r.y &= keep;
+      r.z &= keep;
+      r.w &= keep;
     } else {
       uint32_t h[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        h[i] = (k0 + i < K) ? xrow[k0 + i] : 0u;
+        h[i] = (valid && k0 + i < K) ? row[k0 + i] : 0u;
       }
-      r.x = h[0] | (h[1] << 16);
-      r.y = h[2] | (h[3] << 16);
-      r.z = h[4] | (h[5] << 16);
-      r.w = h[6] | (h[7] << 16);
+      r = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                h[6] | (h[7] << 16)};
     }
+    return __builtin_bit_cast(bf16x8, r);
   }
-  return __builtin_bit_cast(bf16x8, r);
-}
+};
 
+// Sum the waves' partial tiles and store.  Thread o finishes outputs
+// (m, n = o % 16); `scale` is that column's row scale (1 for AQ4), loaded by
+// the caller at kernel start so no memory round trip sits in the epilogue.
 template <int MT, int WAVES>
 __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
                                                  f32x4 (&acc)[MT], float *red,
-                                                 const float *row_scale) {
+                                                 float scale) {
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
 #pragma unroll
@@ -82,10 +97,7 @@ __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
     const uint32_t m = m_base + mt * 16 + mrow;
     const uint32_t n = T * 16 + ncol;
     if (m < a.m && n < a.n) {
-      if (row_scale != nullptr) {
-        v = row_scale[n] * v;
-      }
-      v = a.alpha * v;
+      v = a.alpha * (scale * v);
       if (a.y_f32) {
         static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
       } else {
@@ -95,26 +107,33 @@ __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
   }
 }
 
-template <int MT, int WAVES>
-__global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_kernel(GemvArgs a,
-                                                                bool vec) {
+// Tiles per batch: all activation reads of a batch are issued first, then all
+// weight-tile loads, so the consumer waits on an in-order counter that lets the
+// remaining tile loads stay in flight.
+template <int MT>
+constexpr int fp8_batch() { return MT == 1 ? 8 : 4; }
+template <int MT>
+constexpr int aq4_batch() { return MT == 1 ? 4 : 2; }
+
+template <int MT, int WAVES, bool VEC>
+__global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_kernel(GemvArgs a) {
+  constexpr int B = fp8_batch<MT>();
   __shared__ float red[WAVES * MT * 4 * kWave];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const uint32_t T = blockIdx.x;
+  const float rscale =
+      static_cast<const float *>(a.aux)[T * 16 + threadIdx.x % 16];
   const uint32_t units = a.units;
   const uint32_t ub = uint32_t(uint64_t(units) * wave / WAVES);
   const uint32_t ue = uint32_t(uint64_t(units) * (wave + 1) / WAVES);
   const uint8_t *stripe = static_cast<const uint8_t *>(a.tiles) +
                           uint64_t(T) * units * 1024 + lane * 16;
-
-  const uint16_t *xrow[MT];
-  bool valid[MT];
+  XRow<VEC> xr[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = blockIdx.y * 32 + mt * 16 + lane % 16;
-    valid[mt] = m < a.m;
-    xrow[mt] = a.x + uint64_t(valid[mt] ? m : 0) * a.ldx;
+    xr[mt] = XRow<VEC>(a.x, a.ldx, blockIdx.y * 32 + mt * 16 + lane % 16, a.m,
+                       a.k);
   }
   f32x4 acc[MT];
 #pragma unroll
@@ -123,45 +142,63 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_kernel(GemvArgs a,
   }
   const uint32_t kl = 16 * (lane / 16);
 
-  auto consume = [&](u32x4 wv, uint32_t u) {
+  auto consume = [&](u32x4 wv, const bf16x8 (&xa)[MT][2]) {
     const u32x2 b01 = e4m3x4_to_bf16x4(wv.x);
     const u32x2 b23 = e4m3x4_to_bf16x4(wv.y);
     const u32x2 b45 = e4m3x4_to_bf16x4(wv.z);
     const u32x2 b67 = e4m3x4_to_bf16x4(wv.w);
     const bf16x8 b0 = __builtin_bit_cast(bf16x8, u32x4{b01.x, b01.y, b23.x, b23.y});
     const bf16x8 b1 = __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt] = mfma_bf16(xa[mt][0], b0, acc[mt]);
+      acc[mt] = mfma_bf16(xa[mt][1], b1, acc[mt]);
+    }
+  };
+  auto load_x = [&](uint32_t u, bf16x8 (&xa)[MT][2]) {
     const uint32_t k0 = u * 64 + kl;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const bf16x8 a0 = load_x8(xrow[mt], valid[mt], k0, a.k, vec);
-      const bf16x8 a1 = load_x8(xrow[mt], valid[mt], k0 + 8, a.k, vec);
-      acc[mt] = mfma_bf16(a0, b0, acc[mt]);
-      acc[mt] = mfma_bf16(a1, b1, acc[mt]);
+      xa[mt][0] = xr[mt].load8(k0);
+      xa[mt][1] = xr[mt].load8(k0 + 8);
     }
   };
 
   uint32_t u = ub;
-  for (; u + kBatch <= ue; u += kBatch) {
-    u32x4 wv[kBatch];
+  for (; u + B <= ue; u += B) {
+    bf16x8 xa[B][MT][2];
+    u32x4 wv[B];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      wv[i] = *reinterpret_cast<const u32x4 *>(stripe + uint64_t(u + i) * 1024);
+    for (int i = 0; i < B; ++i) {
+      load_x(u + i, xa[i]);
     }
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      consume(wv[i], u + i);
+    for (int i = 0; i < B; ++i) {
+      wv[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(stripe + uint64_t(u + i) * 1024));
+    }
+    // Keep the whole batch of loads ahead of the first use: without this
+    // fence the scheduler interleaves loads with their consumers and leaves
+    // only one or two tiles in flight.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      consume(wv[i], xa[i]);
     }
   }
   for (; u < ue; ++u) {
-    consume(*reinterpret_cast<const u32x4 *>(stripe + uint64_t(u) * 1024), u);
+    bf16x8 xa[MT][2];
+    load_x(u, xa);
+    consume(__builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(stripe + uint64_t(u) * 1024)),
+            xa);
   }
-  reduce_and_store<MT, WAVES>(a, acc, red,
-                              static_cast<const float *>(a.aux));
+  reduce_and_store<MT, WAVES>(a, acc, red, rscale);
 }
 
-template <int MT, int WAVES>
-__global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a,
-                                                                bool vec) {
+template <int MT, int WAVES, bool VEC>
+__global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a) {
+  constexpr int B = aq4_batch<MT>();
   __shared__ float red[WAVES * MT * 4 * kWave];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -173,14 +210,11 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a,
                            uint64_t(T) * groups * 256 + lane * 4;
   const uint32_t *szs = static_cast<const uint32_t *>(a.aux) +
                         uint64_t(T) * groups * 16 + lane % 16;
-
-  const uint16_t *xrow[MT];
-  bool valid[MT];
+  XRow<VEC> xr[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = blockIdx.y * 32 + mt * 16 + lane % 16;
-    valid[mt] = m < a.m;
-    xrow[mt] = a.x + uint64_t(valid[mt] ? m : 0) * a.ldx;
+    xr[mt] = XRow<VEC>(a.x, a.ldx, blockIdx.y * 32 + mt * 16 + lane % 16, a.m,
+                       a.k);
   }
   f32x4 acc[MT];
 #pragma unroll
@@ -191,7 +225,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a,
   const bf16x8 ones = __builtin_bit_cast(
       bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 
-  auto consume = [&](u32x4 wv, uint32_t szv, uint32_t g) {
+  auto consume = [&](u32x4 wv, uint32_t szv, const bf16x8 (&xa)[MT][4]) {
     const bf16x8 b[4] = {nib8_to_bf16_off128(wv.x), nib8_to_bf16_off128(wv.y),
                          nib8_to_bf16_off128(wv.z), nib8_to_bf16_off128(wv.w)};
     const float sf = f16_to_f32(uint16_t(szv & 0xffffu));
@@ -202,10 +236,8 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a,
       f32x4 xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const bf16x8 av =
-            load_x8(xrow[mt], valid[mt], g * 128 + 32 * j + kl, a.k, vec);
-        p = mfma_bf16(av, b[j], p);
-        xs = mfma_bf16(av, ones, xs);
+        p = mfma_bf16(xa[mt][j], b[j], p);
+        xs = mfma_bf16(xa[mt][j], ones, xs);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -213,31 +245,384 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a,
       }
     }
   };
+  auto load_x = [&](uint32_t g, bf16x8 (&xa)[MT][4]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xa[mt][j] = xr[mt].load8(g * 128 + 32 * j + kl);
+      }
+    }
+  };
 
   uint32_t g = ub;
-  for (; g + kBatch <= ue; g += kBatch) {
-    u32x4 wv[kBatch];
-    uint32_t szv[kBatch];
+  for (; g + B <= ue; g += B) {
+    bf16x8 xa[B][MT][4];
+    u32x4 wv[B];
+    uint32_t szv[B];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      wv[i] = *reinterpret_cast<const u32x4 *>(stripe + uint64_t(g + i) * 256);
-      szv[i] = szs[uint64_t(g + i) * 16];
+    for (int i = 0; i < B; ++i) {
+      load_x(g + i, xa[i]);
     }
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      consume(wv[i], szv[i], g + i);
+    for (int i = 0; i < B; ++i) {
+      szv[i] = szs[uint64_t(g + i) * 16];
+      wv[i] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4 *>(stripe + uint64_t(g + i) * 256));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      consume(wv[i], szv[i], xa[i]);
     }
   }
   for (; g < ue; ++g) {
-    consume(*reinterpret_cast<const u32x4 *>(stripe + uint64_t(g) * 256),
-            szs[uint64_t(g) * 16], g);
+    bf16x8 xa[MT][4];
+    load_x(g, xa);
+    const uint32_t szv = szs[uint64_t(g) * 16];
+    consume(__builtin_nontemporal_load(
+                reinterpret_cast<const u32x4 *>(stripe + uint64_t(g) * 256)),
+            szv, xa);
   }
-  reduce_and_store<MT, WAVES>(a, acc, red, nullptr);
+  reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged variant.  When the workgroup's activation block (rows x K bf16)
+// fits in 64 KiB, it is copied once into LDS with direct global->LDS loads
+// (no registers) issued ahead of the first weight batch, and every MFMA A
+// operand is read from LDS.  Waves then hold only weight tiles in registers:
+// a batch is consumed while the next batch is already in flight.  Rows are
+// stored as 16-byte chunks, chunk c of row r at slot c ^ (r & 7), which
+// spreads the 16 rows an A read touches over different banks.
+constexpr uint32_t kXLdsBytes = 64 * 1024;
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+// Workgroup barrier without the memory fence of __syncthreads (which would
+// drain every outstanding weight load); LDS hazards are covered by the
+// explicit counter waits before it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) |
+                             (0xf << 8));
+}
+
+__device__ __forceinline__ uint32_t x_slot(uint32_t r, uint32_t c,
+                                           uint32_t cpr) {
+  return r * cpr + (c ^ (r & 7u));
+}
+
+// Copy rows [m0, m0 + rows) of x into LDS (slot layout above) and zero one
+// extra row after them; lanes whose row is past M read that zero row, so no
+// A read needs masking.  Each wave DMA instruction fills 64 consecutive
+// slots; lane L's slot maps back to its global chunk through the swizzle.
+template <int WAVES>
+__device__ __forceinline__ void stage_x_lds(const GemvArgs &a, uint16_t *xs,
+                                            uint32_t rows, uint32_t cpr) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t total = rows * cpr;
+  const uint32_t m0 = blockIdx.y * 32;
+  for (uint32_t base = wave * kWave; base < total; base += WAVES * kWave) {
+    const uint32_t p = base + lane;
+    if (p < total) {
+      const uint32_t r = p / cpr;
+      const uint32_t c = (p % cpr) ^ (r & 7u);
+      const uint16_t *src = a.x + uint64_t(m0 + r) * a.ldx + c * 8;
+      __builtin_amdgcn_global_load_lds(
+          (__attribute__((address_space(1))) void *)(src),
+          (__attribute__((address_space(3))) void *)(xs + base * 8), 16, 0, 0);
+    }
+  }
+  for (uint32_t c = threadIdx.x; c < cpr; c += WAVES * kWave) {
+    *reinterpret_cast<u32x4 *>(xs + (total + c) * 8) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <int MT, int WAVES, int B, bool FULL>
+__global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_lds_kernel(
+    GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  __shared__ float red[WAVES * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t T = blockIdx.x;
+  const uint32_t units = a.units;
+  const uint32_t ub = uint32_t(uint64_t(units) * wave / WAVES);
+  const uint32_t ue = uint32_t(uint64_t(units) * (wave + 1) / WAVES);
+  const u32x4 *stripe = reinterpret_cast<const u32x4 *>(
+      static_cast<const uint8_t *>(a.tiles) + uint64_t(T) * units * 1024 +
+      lane * 16);
+  const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
+  const uint32_t cpr = a.k / 8;
+
+  // Activations first (L2-resident, they land early), then the weights.
+  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  __builtin_amdgcn_sched_barrier(0);
+  const float rscale = static_cast<const float *>(a.aux)[T * 16 + threadIdx.x % 16];
+  // Tile indices are clamped into [ub, ue - 1] (tile 0 for a wave with no
+  // tiles) so every load stays inside this stripe.
+  const uint32_t last = ue > ub ? ue - 1 : 0;
+  u32x4 cur[B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    cur[i] = __builtin_nontemporal_load(stripe + uint64_t(min(ub + i, last)) * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<B + 1>();  // this thread's activation copies have landed
+  lds_barrier();
+
+  // A operand of unit u, half h: 8 bf16 at chunk 8u + 2(lane/16) + h.
+  const uint32_t cg = 2 * (lane / 16);
+  const char *xa[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t r = m < rows ? m : rows;
+      xa[mt][h] = reinterpret_cast<const char *>(xs) +
+                  (r * cpr + ((cg + h) ^ (r & 7u))) * 16;
+    }
+  }
+  // Four independent accumulator chains per m-tile: consecutive MFMAs never
+  // wait on each other's results.
+  f32x4 acc4[4][MT];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc4[c][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  for (uint32_t u = ub; u < ue; u += B) {
+    u32x4 nxt[B];
+    const bool more = u + B < ue;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        nxt[i] = __builtin_nontemporal_load(
+            stripe + uint64_t(min(u + B + i, last)) * 64);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      u32x4 wv = cur[i];
+      if (!FULL) {
+        const uint32_t keep = u + i < ue ? 0xffffffffu : 0u;
+        wv.x &= keep;
+        wv.y &= keep;
+        wv.z &= keep;
+        wv.w &= keep;
+      }
+      const u32x2 b01 = e4m3x4_to_bf16x4(wv.x);
+      const u32x2 b23 = e4m3x4_to_bf16x4(wv.y);
+      const u32x2 b45 = e4m3x4_to_bf16x4(wv.z);
+      const u32x2 b67 = e4m3x4_to_bf16x4(wv.w);
+      const bf16x8 b0 =
+          __builtin_bit_cast(bf16x8, u32x4{b01.x, b01.y, b23.x, b23.y});
+      const bf16x8 b1 =
+          __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
+      const uint32_t off = (FULL ? u + i : min(u + i, last)) * 128;
+      const int ca = 2 * (i & 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8 a0 =
+            *reinterpret_cast<const bf16x8 *>(xa[mt][0] + off);
+        const bf16x8 a1 =
+            *reinterpret_cast<const bf16x8 *>(xa[mt][1] + off);
+        acc4[ca][mt] = mfma_bf16(a0, b0, acc4[ca][mt]);
+        acc4[ca + 1][mt] = mfma_bf16(a1, b1, acc4[ca + 1][mt]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        cur[i] = nxt[i];
+      }
+    }
+  }
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = (acc4[0][mt] + acc4[1][mt]) + (acc4[2][mt] + acc4[3][mt]);
+  }
+  reduce_and_store<MT, WAVES>(a, acc, red, rscale);
+}
+
+// AQ4: the per-(row, group) activation sums sum_k x[m, k] over each 128-k
+// group are formed once per workgroup in LDS, so each group costs four MFMAs
+// plus one fp32 correction:
+//   acc += s * (sum_k (128 + q) x  -  (128 + z) * sum_k x).
+template <int MT, int WAVES, int B, bool FULL>
+__global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
+    GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  __shared__ float red[WAVES * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t T = blockIdx.x;
+  const uint32_t groups = a.units;
+  const uint32_t ub = uint32_t(uint64_t(groups) * wave / WAVES);
+  const uint32_t ue = uint32_t(uint64_t(groups) * (wave + 1) / WAVES);
+  const u32x4 *stripe = reinterpret_cast<const u32x4 *>(
+      static_cast<const uint32_t *>(a.tiles) + uint64_t(T) * groups * 256 +
+      lane * 4);
+  const uint32_t *szs = static_cast<const uint32_t *>(a.aux) +
+                        uint64_t(T) * groups * 16 + lane % 16;
+  const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
+  const uint32_t cpr = a.k / 8;
+  // Group sums follow the activation block and its zero row.
+  float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * cpr * 8);
+
+  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t last = ue > ub ? ue - 1 : 0;
+  u32x4 cur[B];
+  uint32_t csz[B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    const uint32_t g = min(ub + i, last);
+    cur[i] = __builtin_nontemporal_load(stripe + uint64_t(g) * 64);
+    csz[i] = szs[uint64_t(g) * 16];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<2 * B>();  // this thread's activation copies have landed
+  lds_barrier();
+  // 16 lanes per (row, group): lane c sums chunk c (8 values), then a
+  // butterfly over the 16 lanes.  The trip count is uniform across the block.
+  for (uint32_t base = 0; base < rows * groups * 16; base += WAVES * kWave) {
+    const uint32_t i = base + threadIdx.x;
+    const uint32_t item = i / 16, c = i % 16;
+    float sum = 0.0f;
+    if (item < rows * groups) {
+      const uint32_t r = item / groups, g = item % groups;
+      const u32x4 v =
+          *reinterpret_cast<const u32x4 *>(xs + x_slot(r, g * 16 + c, cpr) * 8);
+      sum = ((bits_f32(v.x << 16) + bits_f32(v.x & 0xffff0000u)) +
+             (bits_f32(v.y << 16) + bits_f32(v.y & 0xffff0000u))) +
+            ((bits_f32(v.z << 16) + bits_f32(v.z & 0xffff0000u)) +
+             (bits_f32(v.w << 16) + bits_f32(v.w & 0xffff0000u)));
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      sum += __shfl_xor(sum, off, kWave);
+    }
+    if (item < rows * groups && c == 0) {
+      gsum[item] = sum;
+    }
+  }
+  lds_barrier();
+
+  // A operand of group g, MFMA j: chunk 16g + (lane/16) + 4j of row m.
+  const uint32_t q4 = lane / 16;
+  const char *xa[MT][4];
+  const float *gs[MT][4];  // group-sum row of each accumulator element
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+    const uint32_t r = m < rows ? m : rows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xa[mt][j] = reinterpret_cast<const char *>(xs) +
+                  (r * cpr + ((q4 + 4 * j) ^ (r & 7u))) * 16;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t mr = mt * 16 + 4 * q4 + e;
+      gs[mt][e] = gsum + (mr < rows ? mr : 0) * groups;
+    }
+  }
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t nmask = opaque_u32(0x000f000fu);
+  const uint32_t nmagic = opaque_u32(0x43004300u);
+
+  for (uint32_t g = ub; g < ue; g += B) {
+    u32x4 nxt[B];
+    uint32_t nsz[B];
+    const bool more = g + B < ue;
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const uint32_t gg = min(g + B + i, last);
+        nxt[i] = __builtin_nontemporal_load(stripe + uint64_t(gg) * 64);
+        nsz[i] = szs[uint64_t(gg) * 16];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The batch's groups are independent MFMA chains; issuing them
+    // interleaved (j outer, group inner) hides the accumulate latency.
+    f32x4 p[B][MT];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        p[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const bf16x8 bj = nib8_to_bf16_off128(cur[i][j], nmask, nmagic);
+        const uint32_t off = (FULL ? g + i : min(g + i, last)) * 256;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          p[i][mt] = mfma_bf16(*reinterpret_cast<const bf16x8 *>(xa[mt][j] + off),
+                               bj, p[i][mt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      // A clamped (repeated) tile contributes zero through its scale.
+      const float sf = (FULL || g + i < ue)
+                           ? f16_to_f32(uint16_t(csz[i] & 0xffffu))
+                           : 0.0f;
+      const float zoff = 128.0f + f16_to_f32(uint16_t(csz[i] >> 16));
+      const uint32_t gi = FULL ? g + i : min(g + i, last);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][gi]);
+        }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        cur[i] = nxt[i];
+        csz[i] = nsz[i];
+      }
+    }
+  }
+  reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
 }
 
 // Waves per workgroup: enough that the grid holds ~8 waves per CU on the
 // 256-CU part, and no more waves than tile units to share out.
 int pick_waves(uint64_t stripes, uint64_t mblocks, uint32_t units) {
+  static const int forced = [] {
+    const char *e = std::getenv("ULLM_GEMV_WAVES");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced == 4 || forced == 8 || forced == 16) {
+    return forced;
+  }
   const uint64_t wgs = stripes * mblocks;
   int waves = 4;
   while (waves < 16 && wgs * waves < 2048 && uint32_t(waves * 2) <= units) {
@@ -246,30 +631,74 @@ int pick_waves(uint64_t stripes, uint64_t mblocks, uint32_t units) {
   return waves;
 }
 
+// Tuning override: ULLM_GEMV_LDS=0 disables the LDS-staged variant.
+bool lds_allowed() {
+  static const bool ok = [] {
+    const char *e = std::getenv("ULLM_GEMV_LDS");
+    return !(e && e[0] == '0');
+  }();
+  return ok;
+}
+
+// Activation rows plus the zero row, plus the AQ4 group sums.
+uint32_t lds_bytes(const GemvArgs &a, bool aq4) {
+  const uint32_t rows = min(a.m, 32u);
+  return (rows + 1) * a.k * 2 + (aq4 ? rows * (a.k / 128) * 4 : 0);
+}
+
 template <int MT, int WAVES>
 hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
-  hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES>), grid, dim3(WAVES * kWave),
-                     0, s, a, vec);
+  if (vec && lds_allowed() && lds_bytes(a, false) <= kXLdsBytes) {
+    if (a.units % (WAVES * 8) == 0) {
+      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, 8, true>), grid,
+                         dim3(WAVES * kWave), lds_bytes(a, false), s, a);
+    } else {
+      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, 8, false>), grid,
+                         dim3(WAVES * kWave), lds_bytes(a, false), s, a);
+    }
+  } else if (vec) {
+    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, true>), grid,
+                       dim3(WAVES * kWave), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, false>), grid,
+                       dim3(WAVES * kWave), 0, s, a);
+  }
   return hipGetLastError();
 }
 
 template <int MT, int WAVES>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
-  hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES>), grid, dim3(WAVES * kWave),
-                     0, s, a, vec);
+  if (vec && lds_allowed() && lds_bytes(a, true) <= kXLdsBytes) {
+    if (a.units % (WAVES * 4) == 0) {
+      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, 4, true>), grid,
+                         dim3(WAVES * kWave), lds_bytes(a, true), s, a);
+    } else {
+      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, 4, false>), grid,
+                         dim3(WAVES * kWave), lds_bytes(a, true), s, a);
+    }
+  } else if (vec) {
+    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, true>), grid,
+                       dim3(WAVES * kWave), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, false>), grid,
+                       dim3(WAVES * kWave), 0, s, a);
+  }
   return hipGetLastError();
 }
 
-bool x_vec_ok(const GemvArgs &a) {
-  return (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) && (a.ldx % 8 == 0);
+// Unconditional 16-byte activation reads need aligned rows and, for FP8, a
+// K that fills every 64-wide unit (AQ4 K is always a multiple of 128).
+bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
+  return (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) && (a.ldx % 8 == 0) &&
+         (a.k % unit_k == 0);
 }
 
 }  // namespace
 
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
-  const bool vec = x_vec_ok(a);
+  const bool vec = x_vec_ok(a, 64);
   const int waves = pick_waves(a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
   switch (waves * 2 + (two ? 1 : 0)) {
@@ -283,7 +712,7 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
-  const bool vec = x_vec_ok(a);
+  const bool vec = x_vec_ok(a, 128);
   const int waves = pick_waves(a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
   switch (waves * 2 + (two ? 1 : 0)) {
