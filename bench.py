@@ -149,6 +149,18 @@ def bench_gemm(r, m, n, k, steps, warmup):
             "timing": mode}
 
 
+def measured_traffic(workload):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE and
+    committed under profiles/ (None when no such summary exists)."""
+    path = ROOT / "profiles" / f"{workload}_traffic.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def cpu_baseline(seconds=10.0):
     """The oracle's AQ4 matvec on the host cores, same shape, bounded time."""
     import numpy as np
@@ -180,7 +192,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="aq4,fp8,gemm")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain 256 MiB torch copy (a known-size "
+                         "reference kernel for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.cpu_seconds <= 0:
+        args.cpu_seconds = 0.05
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build's kernels are "
               "single-GPU (see DESIGN.md on sharding); run with --gpus 1",
@@ -196,6 +213,13 @@ def main():
         raise SystemExit(f"HIP backend unavailable: {diag}")
     r = Runner(uh, torch, dev)
     want = set(args.configs.split(","))
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     head = bench_matvec(r, uh.ENCODING_AQ4_G128, 1, 14336, 4096, args.steps,
                         args.warmup)
@@ -240,7 +264,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["GB_s"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["GB_s"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel_us": round(us, 3)},
+                     "traffic": measured_traffic("aq4_gemv_m1_k4096_n14336"),
+                     "kernel_us": round(us, 3),
+                     "kernel": "aq4_gemv_lds_kernel"},
         "cpu_baseline": cpu,
         "configs": configs,
     }

@@ -296,6 +296,18 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a) {
 // stored as 16-byte chunks, chunk c of row r at slot c ^ (r & 7), which
 // spreads the 16 rows an A read touches over different banks.
 constexpr uint32_t kXLdsBytes = 64 * 1024;
+#ifndef ULLM_AQ4_LDS_BATCH
+#define ULLM_AQ4_LDS_BATCH 2
+#endif
+// Tiles per batch of the LDS-staged kernels, chosen by measurement on
+// MI355X: small batches that keep a steady stream of requests in flight
+// beat front-loading a wave's whole share (AQ4 M=1 4096->14336: 8.4 us at
+// 2 groups per batch against 11.2 us at 8).
+constexpr int kAq4LdsBatch = ULLM_AQ4_LDS_BATCH;
+#ifndef ULLM_FP8_LDS_BATCH
+#define ULLM_FP8_LDS_BATCH 4
+#endif
+constexpr int kFp8LdsBatch = ULLM_FP8_LDS_BATCH;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -615,18 +627,20 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
 
 // Waves per workgroup: enough that the grid holds ~8 waves per CU on the
 // 256-CU part, and no more waves than tile units to share out.
-int pick_waves(uint64_t stripes, uint64_t mblocks, uint32_t units) {
+// Waves per workgroup (they split K).  Measured on MI355X: FP8 streams best
+// with 8 waves per stripe at every Llama shape; AQ4 (half the bytes per
+// stripe) with 4 once the grid has enough stripes to fill the chip.
+int pick_waves(bool aq4, uint64_t stripes, uint64_t mblocks, uint32_t units) {
   static const int forced = [] {
     const char *e = std::getenv("ULLM_GEMV_WAVES");
     return e ? std::atoi(e) : 0;
   }();
-  if (forced == 4 || forced == 8 || forced == 16) {
+  if (forced == 2 || forced == 4 || forced == 8 || forced == 16) {
     return forced;
   }
-  const uint64_t wgs = stripes * mblocks;
-  int waves = 4;
-  while (waves < 16 && wgs * waves < 2048 && uint32_t(waves * 2) <= units) {
-    waves *= 2;
+  int waves = aq4 && stripes * mblocks >= 512 ? 4 : 8;
+  while (waves > 2 && uint32_t(waves) > units) {
+    waves /= 2;
   }
   return waves;
 }
@@ -650,12 +664,12 @@ template <int MT, int WAVES>
 hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
   if (vec && lds_allowed() && lds_bytes(a, false) <= kXLdsBytes) {
-    if (a.units % (WAVES * 8) == 0) {
-      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, 8, true>), grid,
-                         dim3(WAVES * kWave), lds_bytes(a, false), s, a);
+    if (a.units % (WAVES * kFp8LdsBatch) == 0) {
+      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, true>),
+                         grid, dim3(WAVES * kWave), lds_bytes(a, false), s, a);
     } else {
-      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, 8, false>), grid,
-                         dim3(WAVES * kWave), lds_bytes(a, false), s, a);
+      hipLaunchKernelGGL((fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, false>),
+                         grid, dim3(WAVES * kWave), lds_bytes(a, false), s, a);
     }
   } else if (vec) {
     hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, true>), grid,
@@ -671,12 +685,12 @@ template <int MT, int WAVES>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
   if (vec && lds_allowed() && lds_bytes(a, true) <= kXLdsBytes) {
-    if (a.units % (WAVES * 4) == 0) {
-      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, 4, true>), grid,
-                         dim3(WAVES * kWave), lds_bytes(a, true), s, a);
+    if (a.units % (WAVES * kAq4LdsBatch) == 0) {
+      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, true>),
+                         grid, dim3(WAVES * kWave), lds_bytes(a, true), s, a);
     } else {
-      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, 4, false>), grid,
-                         dim3(WAVES * kWave), lds_bytes(a, true), s, a);
+      hipLaunchKernelGGL((aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, false>),
+                         grid, dim3(WAVES * kWave), lds_bytes(a, true), s, a);
     }
   } else if (vec) {
     hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, true>), grid,
@@ -699,9 +713,11 @@ bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
 
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 64);
-  const int waves = pick_waves(a.n16 / 16, (a.m + 31) / 32, a.units);
+  const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
   switch (waves * 2 + (two ? 1 : 0)) {
+    case 4: return launch_fp8_t<1, 2>(a, vec, s);
+    case 5: return launch_fp8_t<2, 2>(a, vec, s);
     case 8: return launch_fp8_t<1, 4>(a, vec, s);
     case 9: return launch_fp8_t<2, 4>(a, vec, s);
     case 16: return launch_fp8_t<1, 8>(a, vec, s);
@@ -713,9 +729,11 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
 
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
-  const int waves = pick_waves(a.n16 / 16, (a.m + 31) / 32, a.units);
+  const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
   switch (waves * 2 + (two ? 1 : 0)) {
+    case 4: return launch_aq4_t<1, 2>(a, vec, s);
+    case 5: return launch_aq4_t<2, 2>(a, vec, s);
     case 8: return launch_aq4_t<1, 4>(a, vec, s);
     case 9: return launch_aq4_t<2, 4>(a, vec, s);
     case 16: return launch_aq4_t<1, 8>(a, vec, s);
