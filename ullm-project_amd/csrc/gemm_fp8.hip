@@ -4,10 +4,10 @@
 // XA row-major [M][ldxq] (per-token scales a_m), Q in the FP8 wave-tile
 // layout of layout.hpp (per-row scales s_n), fp32 accumulation.
 //
-// Direct-from-L2 version: every wave loads its operands straight from global
-// memory in MFMA lane order (the weight tiles already are), with no LDS
-// staging.  Correct for every shape; the LDS-pipelined kernel replaces it on
-// the hot shapes.
+// Two kernels: an LDS-pipelined one for M >= 128 with K % 128 == 0 and
+// aligned activation rows (the prefill shapes), and a direct-from-L2 one that
+// loads operands straight from global memory in MFMA lane order for every
+// other shape.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -111,6 +111,198 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-pipelined kernel (v_mfma_f32_16x16x128_f8f6f4, fp8 x fp8).
+//
+// Block tile 256 (m) x 256 (n) x 128 (k), 8 waves in a 2 x 4 grid, each wave
+// owning a 128 x 64 output tile (32 MFMA tiles of 16 x 16), which keeps a wave
+// near 200 registers so two waves share each SIMD and cover each other's LDS
+// and barrier latency.  Both operands are staged as 1 KiB "wave tiles": 16
+// rows x 64 k in MFMA lane order (lane l = row l % 16, 16 bytes at
+// k = 16 * (l / 16)), the order the weights already have in HBM.  A lane's
+// 32-byte MFMA operand is its 16 bytes of the k-block [0, 64) tile followed by
+// those of [64, 128), for A and B alike, so the k pairing matches and every
+// LDS read is a lane-contiguous ds_read_b128 (no bank conflicts).  Global ->
+// LDS moves are direct global_load_lds_dwordx4 (no registers); two 64 KiB
+// stages alternate so the copies of step s + 1 run under the MFMAs of step s.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+
+constexpr uint32_t kGemmBM = 256, kGemmBN = 256, kGemmBK = 128;
+constexpr uint32_t kGemmWaves = 8;
+constexpr uint32_t kGemmStageBytes = 64 * 1024;  // A 32 KiB + B 32 KiB
+constexpr uint32_t kGemmLdsBytes = 2 * kGemmStageBytes;
+constexpr uint32_t kGemmCopies = 32 / kGemmWaves;  // tiles per wave per operand
+
+__device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0,
+                                                          0, 0);
+}
+
+__device__ __forceinline__ void dma16(const void *src, void *lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(
+      (__attribute__((address_space(1))) void *)(src),
+      (__attribute__((address_space(3))) void *)(lds_wave_base), 16, 0, 0);
+}
+
+// Barrier without the fence of __syncthreads: LDS reads of this wave are
+// complete (lgkmcnt 0); the caller has already waited for its copies.
+__device__ __forceinline__ void gemm_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+}
+
+// Per-lane source offsets of one stage, loop-invariant across k-steps: the
+// k-step only moves a uniform base, so the copies address memory as
+// "scalar base + 32-bit lane offset" and keep few vector registers live.
+// A tiles: 16 m-tiles x 2 k-blocks; B tiles: 16 stripes x 2 k-blocks; tile
+// (t, kb) sits at byte (t * 2 + kb) * 1024 of its 32 KiB half.  Rows past M
+// and stripes past N repeat the last valid one; their results are never
+// stored.
+struct StageOffsets {
+  uint32_t a[kGemmCopies];  // from xq + ks * 128
+  uint32_t b[kGemmCopies];  // from tiles + ks * 2048
+};
+
+__device__ __forceinline__ StageOffsets gemm_offsets(const GemmArgs &a,
+                                                     uint32_t m0, uint32_t T0,
+                                                     uint32_t stripes) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  StageOffsets o;
+#pragma unroll
+  for (uint32_t i = 0; i < kGemmCopies; ++i) {
+    const uint32_t tile = i * kGemmWaves + wave;  // 0..31
+    const uint32_t t = tile / 2, kb = tile % 2;
+    const uint32_t m = min(m0 + t * 16 + lane % 16, a.m - 1);
+    o.a[i] = m * uint32_t(a.ldxq) + kb * 64 + (lane / 16) * 16;
+    const uint32_t T = min(T0 + t, stripes - 1);
+    o.b[i] = (T * a.units + kb) * 1024 + lane * 16;
+  }
+  return o;
+}
+
+__device__ __forceinline__ void gemm_stage(const GemmArgs &a,
+                                           const StageOffsets &o, char *st,
+                                           uint32_t ks) {
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint8_t *abase = a.xq + uint64_t(ks) * kGemmBK;
+  const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
+#pragma unroll
+  for (uint32_t i = 0; i < kGemmCopies; ++i) {
+    dma16(abase + o.a[i], st + (i * kGemmWaves + wave) * 1024);
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kGemmCopies; ++i) {
+    dma16(bbase + o.b[i], st + 32 * 1024 + (i * kGemmWaves + wave) * 1024);
+  }
+}
+
+__device__ __forceinline__ i32x8 lds_operand(const char *p) {
+  const u32x4 lo = *reinterpret_cast<const u32x4 *>(p);
+  const u32x4 hi = *reinterpret_cast<const u32x4 *>(p + 1024);
+  const u32x8 v = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  return __builtin_bit_cast(i32x8, v);
+}
+
+__global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
+    GemmArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t mblocks = (a.m + kGemmBM - 1) / kGemmBM;
+  const uint32_t nblocks = (a.n + kGemmBN - 1) / kGemmBN;
+  // Workgroups are dispatched round-robin over the 8 XCDs; when the tile
+  // count divides evenly, give each XCD a contiguous range of tiles so the
+  // workgroups sharing one L2 also share operand tiles.
+  const uint32_t total = mblocks * nblocks;
+  const uint32_t id = blockIdx.x;
+  const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
+  const uint32_t bm = tile % mblocks, bn = tile / mblocks;
+  const uint32_t m0 = bm * kGemmBM;
+  const uint32_t T0 = bn * (kGemmBN / 16);
+  const uint32_t stripes = (a.n + 15) / 16;
+  const uint32_t ksteps = a.k / kGemmBK;
+  const uint32_t wm = wave / 4, wn = wave % 4;  // wave's 128 x 64 sub-tile
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  const StageOffsets so = gemm_offsets(a, m0, T0, stripes);
+  gemm_stage(a, so, lds, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  gemm_barrier();
+
+  for (uint32_t ks = 0; ks < ksteps; ++ks) {
+    const char *cur = lds + (ks & 1) * kGemmStageBytes;
+    if (ks + 1 < ksteps) {
+      gemm_stage(a, so, lds + ((ks + 1) & 1) * kGemmStageBytes, ks + 1);
+    }
+    const char *As = cur + (wm * 8 * 2) * 1024 + lane * 16;
+    const char *Bs = cur + 32 * 1024 + (wn * 4 * 2) * 1024 + lane * 16;
+    i32x8 bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf[j] = lds_operand(Bs + j * 2048);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const i32x8 af = lds_operand(As + i * 2048);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = mfma_fp8_k128(af, bf[j], acc[i][j]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the next stage's copies have landed
+    gemm_barrier();
+  }
+
+  // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each
+  // 16 x 16 tile.  Scales are gathered first (independent loads in flight
+  // together); full tiles store without bounds checks.
+  const uint32_t ncol = lane % 16, rq = 4 * (lane / 16);
+  const uint32_t mw = m0 + wm * 128, nw = (T0 + wn * 4) * 16;
+  float sn[4], sm[8][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sn[j] = a.scales[min(nw + j * 16 + ncol, stripes * 16 - 1)];
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
+    }
+  }
+  const bool full = mw + 128 <= a.m && nw + 64 <= a.n;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t m = mw + i * 16 + rq + r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t n = nw + j * 16 + ncol;
+        const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
+        if (full || (m < a.m && n < a.n)) {
+          if (a.y_f32) {
+            static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
+          } else {
+            static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
+                f32_to_bf16(v);
+          }
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
@@ -132,6 +324,21 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   a.alpha = alpha;
   a.y_f32 = y_f32;
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
+  const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
+                           w->fp8.bytes() < (uint64_t(1) << 32);
+  if (vec && offsets_fit && a.k % kGemmBK == 0 && m >= 128) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(fp8_gemm_lds_kernel),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLdsBytes);
+    if (attr != hipSuccess) {
+      return attr;
+    }
+    const uint32_t tiles = ((m + kGemmBM - 1) / kGemmBM) *
+                           ((a.n + kGemmBN - 1) / kGemmBN);
+    hipLaunchKernelGGL(fp8_gemm_lds_kernel, dim3(tiles), dim3(kGemmWaves * kWave),
+                       kGemmLdsBytes, s, a);
+    return hipGetLastError();
+  }
   const dim3 grid((a.n + 63) / 64, (m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel, grid, dim3(256), 0, s, a, vec);
   return hipGetLastError();
