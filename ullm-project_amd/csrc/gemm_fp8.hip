@@ -53,6 +53,7 @@ struct GemmArgs {
   uint32_t m, n, k, units;
   float alpha;
   bool y_f32;
+  bool y_vec;  // bf16 rows 16-byte aligned: coalesced epilogue stores
 };
 
 // 256 threads, block tile 64 (m) x 64 (n); wave (wm, wn) owns 32 x 32.
@@ -129,9 +130,22 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kGemmBM = 256, kGemmBN = 256, kGemmBK = 128;
-constexpr uint32_t kGemmWaves = 8;
+#ifndef ULLM_GEMM_WAVES_N
+#define ULLM_GEMM_WAVES_N 4
+#endif
+// Wave grid: 2 waves along m, kGemmWN along n; each wave owns a
+// 128 x (256 / kGemmWN) tile.
+constexpr uint32_t kGemmWM = 2, kGemmWN = ULLM_GEMM_WAVES_N;
+constexpr uint32_t kGemmWaves = kGemmWM * kGemmWN;
+constexpr uint32_t kGemmTM = kGemmBM / kGemmWM / 16;  // 16-row m-tiles per wave
+constexpr uint32_t kGemmTN = kGemmBN / kGemmWN / 16;  // 16-column n-tiles per wave
 constexpr uint32_t kGemmStageBytes = 64 * 1024;  // A 32 KiB + B 32 KiB
-constexpr uint32_t kGemmLdsBytes = 2 * kGemmStageBytes;
+// Epilogue staging: each wave's 128 x 64 bf16 tile, rows padded to 72 bf16
+// (144 B) so the 4 row groups of a store hit different banks.
+constexpr uint32_t kGemmOutStride = kGemmTN * 16 + 8;
+constexpr uint32_t kGemmOutBytes = kGemmWaves * kGemmTM * 16 * kGemmOutStride * 2;
+constexpr uint32_t kGemmLdsBytes =
+    kGemmOutBytes > 2 * kGemmStageBytes ? kGemmOutBytes : 2 * kGemmStageBytes;
 constexpr uint32_t kGemmCopies = 32 / kGemmWaves;  // tiles per wave per operand
 
 __device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
@@ -223,13 +237,13 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   const uint32_t T0 = bn * (kGemmBN / 16);
   const uint32_t stripes = (a.n + 15) / 16;
   const uint32_t ksteps = a.k / kGemmBK;
-  const uint32_t wm = wave / 4, wn = wave % 4;  // wave's 128 x 64 sub-tile
+  const uint32_t wm = wave / kGemmWN, wn = wave % kGemmWN;  // wave's sub-tile
 
-  f32x4 acc[8][4];
+  f32x4 acc[kGemmTM][kGemmTN];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kGemmTM; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kGemmTN; ++j) {
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -244,20 +258,26 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
     if (ks + 1 < ksteps) {
       gemm_stage(a, so, lds + ((ks + 1) & 1) * kGemmStageBytes, ks + 1);
     }
-    const char *As = cur + (wm * 8 * 2) * 1024 + lane * 16;
-    const char *Bs = cur + 32 * 1024 + (wn * 4 * 2) * 1024 + lane * 16;
-    i32x8 bf[4];
+    const char *As = cur + (wm * kGemmTM * 2) * 1024 + lane * 16;
+    const char *Bs = cur + 32 * 1024 + (wn * kGemmTN * 2) * 1024 + lane * 16;
+    i32x8 bf[kGemmTN];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kGemmTN; ++j) {
       bf[j] = lds_operand(Bs + j * 2048);
     }
+    // The A operand of m-tile i + 1 is read while the MFMAs of m-tile i run.
+    i32x8 af = lds_operand(As);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const i32x8 af = lds_operand(As + i * 2048);
+    for (int i = 0; i < kGemmTM; ++i) {
+      i32x8 an = af;
+      if (i + 1 < kGemmTM) {
+        an = lds_operand(As + (i + 1) * 2048);
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kGemmTN; ++j) {
         acc[i][j] = mfma_fp8_k128(af, bf[j], acc[i][j]);
       }
+      af = an;
     }
     __builtin_amdgcn_s_waitcnt(0);  // the next stage's copies have landed
     gemm_barrier();
@@ -267,27 +287,70 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   // 16 x 16 tile.  Scales are gathered first (independent loads in flight
   // together); full tiles store without bounds checks.
   const uint32_t ncol = lane % 16, rq = 4 * (lane / 16);
-  const uint32_t mw = m0 + wm * 128, nw = (T0 + wn * 4) * 16;
-  float sn[4], sm[8][4];
+  const uint32_t mw = m0 + wm * kGemmTM * 16, nw = (T0 + wn * kGemmTN) * 16;
+  float sn[kGemmTN], sm[kGemmTM][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kGemmTN; ++j) {
     sn[j] = a.scales[min(nw + j * 16 + ncol, stripes * 16 - 1)];
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kGemmTM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
     }
   }
-  const bool full = mw + 128 <= a.m && nw + 64 <= a.n;
+  if (!a.y_f32 && a.y_vec) {
+    // bf16 out through LDS: scale, round and stage the tile, then write
+    // whole 16-byte row segments (8 rows of 128 B per wave instruction).
+    // The main loop ended on a barrier, so the operand stages are free.
+    uint16_t *tile = reinterpret_cast<uint16_t *>(lds) +
+                     wave * kGemmTM * 16 * kGemmOutStride;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kGemmTM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int j = 0; j < kGemmTN; ++j) {
+          const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
+          tile[(i * 16 + rq + r) * kGemmOutStride + j * 16 + ncol] =
+              f32_to_bf16(v);
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
+    // A wave instruction writes 64 lanes x 16 B: kGemmTN * 2 lanes per row.
+    constexpr uint32_t lpr = kGemmTN * 2, rpi = kWave / lpr;
+    const uint32_t c8 = (lane % lpr) * 8;
+    const uint32_t n = nw + c8;
+#pragma unroll
+    for (uint32_t it = 0; it < kGemmTM * 16 / rpi; ++it) {
+      const uint32_t row = it * rpi + lane / lpr;
+      const uint32_t m = mw + row;
+      const u32x4 v =
+          *reinterpret_cast<const u32x4 *>(tile + row * kGemmOutStride + c8);
+      uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
+      if (m < a.m) {
+        if (n + 8 <= a.n) {
+          *reinterpret_cast<u32x4 *>(dst) = v;
+        } else {
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+          for (uint32_t e = 0; e < 8 && n + e < a.n; ++e) {
+            dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e % 2)));
+          }
+        }
+      }
+    }
+    return;
+  }
+  const bool full = mw + kGemmTM * 16 <= a.m && nw + kGemmTN * 16 <= a.n;
+#pragma unroll
+  for (int i = 0; i < kGemmTM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t m = mw + i * 16 + rq + r;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kGemmTN; ++j) {
         const uint32_t n = nw + j * 16 + ncol;
         const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
         if (full || (m < a.m && n < a.n)) {
@@ -323,6 +386,7 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   a.units = static_cast<uint32_t>(w->fp8.blocks_per_stripe());
   a.alpha = alpha;
   a.y_f32 = y_f32;
+  a.y_vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && ldy % 8 == 0;
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
   const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
                            w->fp8.bytes() < (uint64_t(1) << 32);
