@@ -149,6 +149,27 @@ def bench_gemm(r, m, n, k, steps, warmup):
             "timing": mode}
 
 
+def bench_stack(r, steps, warmup):
+    """BASELINE config #5: 32-layer AQ4 Llama-3-8B-shaped linear stack +
+    lm_head, batch 8 single-token decode; one step = 129 forward calls."""
+    import stack
+    st = stack.DecodeStack(r.uh, r.torch, r.dev, batch=8)
+    g = r.torch.Generator(device=r.dev)
+    g.manual_seed(5)
+    st.h0.copy_(r.torch.randn(st.h0.shape, generator=g, device=r.dev))
+    ms_step, _, mode = r.time_sweep([st.step], steps, warmup)
+    logits = st.logits.float()
+    finite = bool(r.torch.isfinite(logits).all())
+    rms = float(logits.pow(2).mean().sqrt())
+    st.destroy()
+    per = stack.step_bytes()
+    gbs = per / (ms_step * 1e-3) / 1e9
+    return {"layers": 32, "batch": 8, "bytes_per_step": per,
+            "us_per_step": ms_step * 1e3, "GB_s": gbs,
+            "frac_hbm": gbs / HBM_PEAK_GBS, "tokens_per_s": 8 / (ms_step * 1e-3),
+            "logits_finite": finite, "logits_rms": rms, "timing": mode}
+
+
 def measured_traffic(workload):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE and
     committed under profiles/ (None when no such summary exists)."""
@@ -190,7 +211,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="aq4,fp8,gemm")
+    ap.add_argument("--configs", default="aq4,fp8,gemm,stack")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain 256 MiB torch copy (a known-size "
@@ -237,6 +258,9 @@ def main():
                                    max(10, args.steps // 5), 2)
                 configs[f"fp8_sweep_{name}_m{m}"] = res
                 log(name, m, res["GB_s"])
+    if "stack" in want:
+        configs["aq4_stack_32l_batch8"] = bench_stack(r, max(5, args.steps // 5), 2)
+        log("stack:", configs["aq4_stack_32l_batch8"])
     if "gemm" in want:
         configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
             r, 2048, 28672, 4096, max(3, args.steps // 10), 1)

@@ -241,9 +241,9 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
 
   f32x4 acc[kGemmTM][kGemmTN];
 #pragma unroll
-  for (int i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < kGemmTM; ++i) {
 #pragma unroll
-    for (int j = 0; j < kGemmTN; ++j) {
+    for (uint32_t j = 0; j < kGemmTN; ++j) {
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
@@ -262,19 +262,19 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
     const char *Bs = cur + 32 * 1024 + (wn * kGemmTN * 2) * 1024 + lane * 16;
     i32x8 bf[kGemmTN];
 #pragma unroll
-    for (int j = 0; j < kGemmTN; ++j) {
+    for (uint32_t j = 0; j < kGemmTN; ++j) {
       bf[j] = lds_operand(Bs + j * 2048);
     }
     // The A operand of m-tile i + 1 is read while the MFMAs of m-tile i run.
     i32x8 af = lds_operand(As);
 #pragma unroll
-    for (int i = 0; i < kGemmTM; ++i) {
+    for (uint32_t i = 0; i < kGemmTM; ++i) {
       i32x8 an = af;
       if (i + 1 < kGemmTM) {
         an = lds_operand(As + (i + 1) * 2048);
       }
 #pragma unroll
-      for (int j = 0; j < kGemmTN; ++j) {
+      for (uint32_t j = 0; j < kGemmTN; ++j) {
         acc[i][j] = mfma_fp8_k128(af, bf[j], acc[i][j]);
       }
       af = an;
@@ -290,11 +290,11 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   const uint32_t mw = m0 + wm * kGemmTM * 16, nw = (T0 + wn * kGemmTN) * 16;
   float sn[kGemmTN], sm[kGemmTM][4];
 #pragma unroll
-  for (int j = 0; j < kGemmTN; ++j) {
+  for (uint32_t j = 0; j < kGemmTN; ++j) {
     sn[j] = a.scales[min(nw + j * 16 + ncol, stripes * 16 - 1)];
   }
 #pragma unroll
-  for (int i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < kGemmTM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
@@ -307,11 +307,11 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
     uint16_t *tile = reinterpret_cast<uint16_t *>(lds) +
                      wave * kGemmTM * 16 * kGemmOutStride;
 #pragma unroll
-    for (int i = 0; i < kGemmTM; ++i) {
+    for (uint32_t i = 0; i < kGemmTM; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
-        for (int j = 0; j < kGemmTN; ++j) {
+        for (uint32_t j = 0; j < kGemmTN; ++j) {
           const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
           tile[(i * 16 + rq + r) * kGemmOutStride + j * 16 + ncol] =
               f32_to_bf16(v);
@@ -345,12 +345,12 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   }
   const bool full = mw + kGemmTM * 16 <= a.m && nw + kGemmTN * 16 <= a.n;
 #pragma unroll
-  for (int i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < kGemmTM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t m = mw + i * 16 + rq + r;
 #pragma unroll
-      for (int j = 0; j < kGemmTN; ++j) {
+      for (uint32_t j = 0; j < kGemmTN; ++j) {
         const uint32_t n = nw + j * 16 + ncol;
         const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
         if (full || (m < a.m && n < a.n)) {
