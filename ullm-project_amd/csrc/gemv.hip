@@ -633,8 +633,6 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
   reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
 }
 
-// Waves per workgroup: enough that the grid holds ~8 waves per CU on the
-// 256-CU part, and no more waves than tile units to share out.
 // Waves per workgroup (they split K).  Measured on MI355X: FP8 streams best
 // with 8 waves per stripe at every Llama shape; AQ4 (half the bytes per
 // stripe) with 4 once the grid has enough stripes to fill the chip.
