@@ -8,6 +8,8 @@
 // aligned activation rows (the prefill shapes), and a direct-from-L2 one that
 // loads operands straight from global memory in MFMA lane order for every
 // other shape.
+#include <cstdlib>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -115,38 +117,41 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
 // ---------------------------------------------------------------------------
 // LDS-pipelined kernel (v_mfma_f32_16x16x128_f8f6f4, fp8 x fp8).
 //
-// Block tile 256 (m) x 256 (n) x 128 (k), 8 waves in a 2 x 4 grid, each wave
-// owning a 128 x 64 output tile (32 MFMA tiles of 16 x 16), which keeps a wave
-// near 200 registers so two waves share each SIMD and cover each other's LDS
-// and barrier latency.  Both operands are staged as 1 KiB "wave tiles": 16
-// rows x 64 k in MFMA lane order (lane l = row l % 16, 16 bytes at
-// k = 16 * (l / 16)), the order the weights already have in HBM.  A lane's
-// 32-byte MFMA operand is its 16 bytes of the k-block [0, 64) tile followed by
-// those of [64, 128), for A and B alike, so the k pairing matches and every
-// LDS read is a lane-contiguous ds_read_b128 (no bank conflicts).  Global ->
-// LDS moves are direct global_load_lds_dwordx4 (no registers); two 64 KiB
-// stages alternate so the copies of step s + 1 run under the MFMAs of step s.
+// Block tile BM x BN x 128 (k), WM x WN waves, each wave owning a
+// (BM / WM) x (BN / WN) output tile of 16 x 16 MFMA tiles.  Both operands are
+// staged as 1 KiB "wave tiles": 16 rows x 64 k in MFMA lane order (lane l =
+// row l % 16, 16 bytes at k = 16 * (l / 16)), the order the weights already
+// have in HBM.  A lane's 32-byte MFMA operand is its 16 bytes of the k-block
+// [0, 64) tile followed by those of [64, 128), for A and B alike, so the k
+// pairing matches and every LDS read is a lane-contiguous ds_read_b128 (no
+// bank conflicts).  Global -> LDS moves are direct global_load_lds_dwordx4
+// (no registers); two stages alternate so the copies of step s + 1 run under
+// the MFMAs of step s.  The default 256 x 256 block (8 waves of 128 x 64)
+// measured fastest on MI355X: 1.77 PFLOP/s at M=2048, N=28672, K=4096 with
+// random operands, against 1.37 for a 128 x 128 block that fits two
+// workgroups per CU but doubles the operand traffic from L2.
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
-constexpr uint32_t kGemmBM = 256, kGemmBN = 256, kGemmBK = 128;
-#ifndef ULLM_GEMM_WAVES_N
-#define ULLM_GEMM_WAVES_N 4
-#endif
-// Wave grid: 2 waves along m, kGemmWN along n; each wave owns a
-// 128 x (256 / kGemmWN) tile.
-constexpr uint32_t kGemmWM = 2, kGemmWN = ULLM_GEMM_WAVES_N;
-constexpr uint32_t kGemmWaves = kGemmWM * kGemmWN;
-constexpr uint32_t kGemmTM = kGemmBM / kGemmWM / 16;  // 16-row m-tiles per wave
-constexpr uint32_t kGemmTN = kGemmBN / kGemmWN / 16;  // 16-column n-tiles per wave
-constexpr uint32_t kGemmStageBytes = 64 * 1024;  // A 32 KiB + B 32 KiB
-// Epilogue staging: each wave's 128 x 64 bf16 tile, rows padded to 72 bf16
-// (144 B) so the 4 row groups of a store hit different banks.
-constexpr uint32_t kGemmOutStride = kGemmTN * 16 + 8;
-constexpr uint32_t kGemmOutBytes = kGemmWaves * kGemmTM * 16 * kGemmOutStride * 2;
-constexpr uint32_t kGemmLdsBytes =
-    kGemmOutBytes > 2 * kGemmStageBytes ? kGemmOutBytes : 2 * kGemmStageBytes;
-constexpr uint32_t kGemmCopies = 32 / kGemmWaves;  // tiles per wave per operand
+template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_>
+struct GemmCfg {
+  static constexpr uint32_t BM = BM_, BN = BN_, BK = 128, WM = WM_, WN = WN_;
+  static constexpr uint32_t WAVES = WM * WN;
+  static constexpr uint32_t TM = BM / WM / 16;  // 16-row m-tiles per wave
+  static constexpr uint32_t TN = BN / WN / 16;  // 16-column n-tiles per wave
+  static constexpr uint32_t A_TILES = BM / 16 * 2, B_TILES = BN / 16 * 2;
+  static constexpr uint32_t A_BYTES = A_TILES * 1024;
+  static constexpr uint32_t STAGE = (A_TILES + B_TILES) * 1024;
+  static constexpr uint32_t A_COPIES = A_TILES / WAVES;
+  static constexpr uint32_t B_COPIES = B_TILES / WAVES;
+  static_assert(A_TILES % WAVES == 0 && B_TILES % WAVES == 0, "copy split");
+  // Epilogue staging of each wave's bf16 tile; rows padded by 16 bytes so
+  // the row groups of one LDS store land in different banks.
+  static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
+  static constexpr uint32_t OUT_BYTES = WAVES * TM * 16 * OUT_STRIDE * 2;
+  static constexpr uint32_t LDS = OUT_BYTES > 2 * STAGE ? OUT_BYTES : 2 * STAGE;
+  static_assert(kWave % (TN * 2) == 0, "epilogue row split");
+};
 
 __device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0,
@@ -166,52 +171,6 @@ __device__ __forceinline__ void gemm_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
-// Per-lane source offsets of one stage, loop-invariant across k-steps: the
-// k-step only moves a uniform base, so the copies address memory as
-// "scalar base + 32-bit lane offset" and keep few vector registers live.
-// A tiles: 16 m-tiles x 2 k-blocks; B tiles: 16 stripes x 2 k-blocks; tile
-// (t, kb) sits at byte (t * 2 + kb) * 1024 of its 32 KiB half.  Rows past M
-// and stripes past N repeat the last valid one; their results are never
-// stored.
-struct StageOffsets {
-  uint32_t a[kGemmCopies];  // from xq + ks * 128
-  uint32_t b[kGemmCopies];  // from tiles + ks * 2048
-};
-
-__device__ __forceinline__ StageOffsets gemm_offsets(const GemmArgs &a,
-                                                     uint32_t m0, uint32_t T0,
-                                                     uint32_t stripes) {
-  const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
-  StageOffsets o;
-#pragma unroll
-  for (uint32_t i = 0; i < kGemmCopies; ++i) {
-    const uint32_t tile = i * kGemmWaves + wave;  // 0..31
-    const uint32_t t = tile / 2, kb = tile % 2;
-    const uint32_t m = min(m0 + t * 16 + lane % 16, a.m - 1);
-    o.a[i] = m * uint32_t(a.ldxq) + kb * 64 + (lane / 16) * 16;
-    const uint32_t T = min(T0 + t, stripes - 1);
-    o.b[i] = (T * a.units + kb) * 1024 + lane * 16;
-  }
-  return o;
-}
-
-__device__ __forceinline__ void gemm_stage(const GemmArgs &a,
-                                           const StageOffsets &o, char *st,
-                                           uint32_t ks) {
-  const uint32_t wave = threadIdx.x / kWave;
-  const uint8_t *abase = a.xq + uint64_t(ks) * kGemmBK;
-  const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
-#pragma unroll
-  for (uint32_t i = 0; i < kGemmCopies; ++i) {
-    dma16(abase + o.a[i], st + (i * kGemmWaves + wave) * 1024);
-  }
-#pragma unroll
-  for (uint32_t i = 0; i < kGemmCopies; ++i) {
-    dma16(bbase + o.b[i], st + 32 * 1024 + (i * kGemmWaves + wave) * 1024);
-  }
-}
-
 __device__ __forceinline__ i32x8 lds_operand(const char *p) {
   const u32x4 lo = *reinterpret_cast<const u32x4 *>(p);
   const u32x4 hi = *reinterpret_cast<const u32x4 *>(p + 1024);
@@ -219,13 +178,14 @@ __device__ __forceinline__ i32x8 lds_operand(const char *p) {
   return __builtin_bit_cast(i32x8, v);
 }
 
-__global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
+template <class C>
+__global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = threadIdx.x / kWave;
-  const uint32_t mblocks = (a.m + kGemmBM - 1) / kGemmBM;
-  const uint32_t nblocks = (a.n + kGemmBN - 1) / kGemmBN;
+  const uint32_t mblocks = (a.m + C::BM - 1) / C::BM;
+  const uint32_t nblocks = (a.n + C::BN - 1) / C::BN;
   // Workgroups are dispatched round-robin over the 8 XCDs; when the tile
   // count divides evenly, give each XCD a contiguous range of tiles so the
   // workgroups sharing one L2 also share operand tiles.
@@ -233,48 +193,78 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   const uint32_t id = blockIdx.x;
   const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
   const uint32_t bm = tile % mblocks, bn = tile / mblocks;
-  const uint32_t m0 = bm * kGemmBM;
-  const uint32_t T0 = bn * (kGemmBN / 16);
+  const uint32_t m0 = bm * C::BM;
+  const uint32_t T0 = bn * (C::BN / 16);
   const uint32_t stripes = (a.n + 15) / 16;
-  const uint32_t ksteps = a.k / kGemmBK;
-  const uint32_t wm = wave / kGemmWN, wn = wave % kGemmWN;  // wave's sub-tile
+  const uint32_t ksteps = a.k / C::BK;
+  const uint32_t wm = wave / C::WN, wn = wave % C::WN;
 
-  f32x4 acc[kGemmTM][kGemmTN];
+  // Per-lane copy sources, loop-invariant: a k-step only moves a uniform
+  // base, so copies address memory as "scalar base + 32-bit lane offset".
+  // Tile (t, kb) of an operand sits at byte (t * 2 + kb) * 1024 of its half
+  // of the stage.  Rows past M and stripes past N repeat the last valid one;
+  // their results are never stored.
+  uint32_t aoff[C::A_COPIES], boff[C::B_COPIES];
 #pragma unroll
-  for (uint32_t i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < C::A_COPIES; ++i) {
+    const uint32_t t = (i * C::WAVES + wave) / 2, kb = (i * C::WAVES + wave) % 2;
+    const uint32_t m = min(m0 + t * 16 + lane % 16, a.m - 1);
+    aoff[i] = m * uint32_t(a.ldxq) + kb * 64 + (lane / 16) * 16;
+  }
 #pragma unroll
-    for (uint32_t j = 0; j < kGemmTN; ++j) {
+  for (uint32_t i = 0; i < C::B_COPIES; ++i) {
+    const uint32_t t = (i * C::WAVES + wave) / 2, kb = (i * C::WAVES + wave) % 2;
+    const uint32_t T = min(T0 + t, stripes - 1);
+    boff[i] = (T * a.units + kb) * 1024 + lane * 16;
+  }
+  auto stage = [&](char *st, uint32_t ks) {
+    const uint8_t *abase = a.xq + uint64_t(ks) * C::BK;
+    const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
+#pragma unroll
+    for (uint32_t i = 0; i < C::A_COPIES; ++i) {
+      dma16(abase + aoff[i], st + (i * C::WAVES + wave) * 1024);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < C::B_COPIES; ++i) {
+      dma16(bbase + boff[i], st + C::A_BYTES + (i * C::WAVES + wave) * 1024);
+    }
+  };
+
+  f32x4 acc[C::TM][C::TN];
+#pragma unroll
+  for (uint32_t i = 0; i < C::TM; ++i) {
+#pragma unroll
+    for (uint32_t j = 0; j < C::TN; ++j) {
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
 
-  const StageOffsets so = gemm_offsets(a, m0, T0, stripes);
-  gemm_stage(a, so, lds, 0);
+  stage(lds, 0);
   __builtin_amdgcn_s_waitcnt(0);
   gemm_barrier();
 
   for (uint32_t ks = 0; ks < ksteps; ++ks) {
-    const char *cur = lds + (ks & 1) * kGemmStageBytes;
+    const char *cur = lds + (ks & 1) * C::STAGE;
     if (ks + 1 < ksteps) {
-      gemm_stage(a, so, lds + ((ks + 1) & 1) * kGemmStageBytes, ks + 1);
+      stage(lds + ((ks + 1) & 1) * C::STAGE, ks + 1);
     }
-    const char *As = cur + (wm * kGemmTM * 2) * 1024 + lane * 16;
-    const char *Bs = cur + 32 * 1024 + (wn * kGemmTN * 2) * 1024 + lane * 16;
-    i32x8 bf[kGemmTN];
+    const char *As = cur + (wm * C::TM * 2) * 1024 + lane * 16;
+    const char *Bs = cur + C::A_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
+    i32x8 bf[C::TN];
 #pragma unroll
-    for (uint32_t j = 0; j < kGemmTN; ++j) {
+    for (uint32_t j = 0; j < C::TN; ++j) {
       bf[j] = lds_operand(Bs + j * 2048);
     }
     // The A operand of m-tile i + 1 is read while the MFMAs of m-tile i run.
     i32x8 af = lds_operand(As);
 #pragma unroll
-    for (uint32_t i = 0; i < kGemmTM; ++i) {
+    for (uint32_t i = 0; i < C::TM; ++i) {
       i32x8 an = af;
-      if (i + 1 < kGemmTM) {
+      if (i + 1 < C::TM) {
         an = lds_operand(As + (i + 1) * 2048);
       }
 #pragma unroll
-      for (uint32_t j = 0; j < kGemmTN; ++j) {
+      for (uint32_t j = 0; j < C::TN; ++j) {
         acc[i][j] = mfma_fp8_k128(af, bf[j], acc[i][j]);
       }
       af = an;
@@ -285,16 +275,16 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
 
   // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each
   // 16 x 16 tile.  Scales are gathered first (independent loads in flight
-  // together); full tiles store without bounds checks.
+  // together).
   const uint32_t ncol = lane % 16, rq = 4 * (lane / 16);
-  const uint32_t mw = m0 + wm * kGemmTM * 16, nw = (T0 + wn * kGemmTN) * 16;
-  float sn[kGemmTN], sm[kGemmTM][4];
+  const uint32_t mw = m0 + wm * C::TM * 16, nw = (T0 + wn * C::TN) * 16;
+  float sn[C::TN], sm[C::TM][4];
 #pragma unroll
-  for (uint32_t j = 0; j < kGemmTN; ++j) {
+  for (uint32_t j = 0; j < C::TN; ++j) {
     sn[j] = a.scales[min(nw + j * 16 + ncol, stripes * 16 - 1)];
   }
 #pragma unroll
-  for (uint32_t i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
@@ -302,33 +292,32 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
   }
   if (!a.y_f32 && a.y_vec) {
     // bf16 out through LDS: scale, round and stage the tile, then write
-    // whole 16-byte row segments (8 rows of 128 B per wave instruction).
-    // The main loop ended on a barrier, so the operand stages are free.
-    uint16_t *tile = reinterpret_cast<uint16_t *>(lds) +
-                     wave * kGemmTM * 16 * kGemmOutStride;
+    // whole 16-byte row segments.  The main loop ended on a barrier, so the
+    // operand stages are free.
+    uint16_t *tile_out = reinterpret_cast<uint16_t *>(lds) +
+                         wave * C::TM * 16 * C::OUT_STRIDE;
 #pragma unroll
-    for (uint32_t i = 0; i < kGemmTM; ++i) {
+    for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
-        for (uint32_t j = 0; j < kGemmTN; ++j) {
+        for (uint32_t j = 0; j < C::TN; ++j) {
           const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
-          tile[(i * 16 + rq + r) * kGemmOutStride + j * 16 + ncol] =
+          tile_out[(i * 16 + rq + r) * C::OUT_STRIDE + j * 16 + ncol] =
               f32_to_bf16(v);
         }
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
-    // A wave instruction writes 64 lanes x 16 B: kGemmTN * 2 lanes per row.
-    constexpr uint32_t lpr = kGemmTN * 2, rpi = kWave / lpr;
+    constexpr uint32_t lpr = C::TN * 2, rpi = kWave / lpr;
     const uint32_t c8 = (lane % lpr) * 8;
     const uint32_t n = nw + c8;
 #pragma unroll
-    for (uint32_t it = 0; it < kGemmTM * 16 / rpi; ++it) {
+    for (uint32_t it = 0; it < C::TM * 16 / rpi; ++it) {
       const uint32_t row = it * rpi + lane / lpr;
       const uint32_t m = mw + row;
-      const u32x4 v =
-          *reinterpret_cast<const u32x4 *>(tile + row * kGemmOutStride + c8);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(
+          tile_out + row * C::OUT_STRIDE + c8);
       uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
       if (m < a.m) {
         if (n + 8 <= a.n) {
@@ -343,14 +332,14 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
     }
     return;
   }
-  const bool full = mw + kGemmTM * 16 <= a.m && nw + kGemmTN * 16 <= a.n;
+  const bool full = mw + C::TM * 16 <= a.m && nw + C::TN * 16 <= a.n;
 #pragma unroll
-  for (uint32_t i = 0; i < kGemmTM; ++i) {
+  for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t m = mw + i * 16 + rq + r;
 #pragma unroll
-      for (uint32_t j = 0; j < kGemmTN; ++j) {
+      for (uint32_t j = 0; j < C::TN; ++j) {
         const uint32_t n = nw + j * 16 + ncol;
         const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
         if (full || (m < a.m && n < a.n)) {
@@ -364,6 +353,33 @@ __global__ __launch_bounds__(kGemmWaves *kWave, 1) void fp8_gemm_lds_kernel(
       }
     }
   }
+}
+
+using GemmLarge = GemmCfg<256, 256, 2, 4>;  // default: 1 workgroup per CU
+using GemmMid = GemmCfg<128, 128, 2, 2>;    // 2 workgroups per CU
+
+template <class C>
+hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(C::LDS));
+  if (attr != hipSuccess) {
+    return attr;
+  }
+  const uint32_t tiles =
+      ((a.m + C::BM - 1) / C::BM) * ((a.n + C::BN - 1) / C::BN);
+  hipLaunchKernelGGL(fp8_gemm_lds_kernel<C>, dim3(tiles), dim3(C::WAVES * kWave),
+                     C::LDS, s, a);
+  return hipGetLastError();
+}
+
+// Tuning override: ULLM_GEMM_CFG=mid selects the 128 x 128 block.
+bool gemm_mid_forced() {
+  static const bool v = [] {
+    const char *e = std::getenv("ULLM_GEMM_CFG");
+    return e != nullptr && e[0] == 'm';
+  }();
+  return v;
 }
 
 }  // namespace
@@ -390,18 +406,9 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
   const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
                            w->fp8.bytes() < (uint64_t(1) << 32);
-  if (vec && offsets_fit && a.k % kGemmBK == 0 && m >= 128) {
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(fp8_gemm_lds_kernel),
-        hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLdsBytes);
-    if (attr != hipSuccess) {
-      return attr;
-    }
-    const uint32_t tiles = ((m + kGemmBM - 1) / kGemmBM) *
-                           ((a.n + kGemmBN - 1) / kGemmBN);
-    hipLaunchKernelGGL(fp8_gemm_lds_kernel, dim3(tiles), dim3(kGemmWaves * kWave),
-                       kGemmLdsBytes, s, a);
-    return hipGetLastError();
+  if (vec && offsets_fit && a.k % 128 == 0 && m >= 128) {
+    return gemm_mid_forced() ? launch_gemm_lds<GemmMid>(a, s)
+                             : launch_gemm_lds<GemmLarge>(a, s);
   }
   const dim3 grid((a.n + 63) / 64, (m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel, grid, dim3(256), 0, s, a, vec);
