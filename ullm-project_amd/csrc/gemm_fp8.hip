@@ -133,15 +133,24 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
-template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_>
+#ifndef ULLM_GEMM_BSTAGES
+#define ULLM_GEMM_BSTAGES 2
+#endif
+
+template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_,
+          uint32_t BSTAGES_ = 2>
 struct GemmCfg {
   static constexpr uint32_t BM = BM_, BN = BN_, BK = 128, WM = WM_, WN = WN_;
+  // A (activations, L2-resident) is double-buffered; B (weights, streamed
+  // from HBM) may get a third buffer so its copies run two k-steps ahead.
+  static constexpr uint32_t BSTAGES = BSTAGES_;
   static constexpr uint32_t WAVES = WM * WN;
   static constexpr uint32_t TM = BM / WM / 16;  // 16-row m-tiles per wave
   static constexpr uint32_t TN = BN / WN / 16;  // 16-column n-tiles per wave
   static constexpr uint32_t A_TILES = BM / 16 * 2, B_TILES = BN / 16 * 2;
   static constexpr uint32_t A_BYTES = A_TILES * 1024;
-  static constexpr uint32_t STAGE = (A_TILES + B_TILES) * 1024;
+  static constexpr uint32_t B_BYTES = B_TILES * 1024;
+  static constexpr uint32_t STAGE_BYTES = 2 * A_BYTES + BSTAGES * B_BYTES;
   static constexpr uint32_t A_COPIES = A_TILES / WAVES;
   static constexpr uint32_t B_COPIES = B_TILES / WAVES;
   static_assert(A_TILES % WAVES == 0 && B_TILES % WAVES == 0, "copy split");
@@ -149,7 +158,9 @@ struct GemmCfg {
   // the row groups of one LDS store land in different banks.
   static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
   static constexpr uint32_t OUT_BYTES = WAVES * TM * 16 * OUT_STRIDE * 2;
-  static constexpr uint32_t LDS = OUT_BYTES > 2 * STAGE ? OUT_BYTES : 2 * STAGE;
+  static constexpr uint32_t LDS =
+      OUT_BYTES > STAGE_BYTES ? OUT_BYTES : STAGE_BYTES;
+  static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
   static_assert(kWave % (TN * 2) == 0, "epilogue row split");
 };
 
@@ -169,6 +180,15 @@ __device__ __forceinline__ void dma16(const void *src, void *lds_wave_base) {
 __device__ __forceinline__ void gemm_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_s_barrier();
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) |
+                             (0xf << 8));
 }
 
 __device__ __forceinline__ i32x8 lds_operand(const char *p) {
@@ -217,18 +237,28 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     const uint32_t T = min(T0 + t, stripes - 1);
     boff[i] = (T * a.units + kb) * 1024 + lane * 16;
   }
-  auto stage = [&](char *st, uint32_t ks) {
+  // LDS: A buffers [0, 2 * A_BYTES), then BSTAGES B buffers.
+  auto a_buf = [&](uint32_t ks) { return lds + (ks & 1) * C::A_BYTES; };
+  auto b_buf = [&](uint32_t ks) {
+    return lds + 2 * C::A_BYTES + (ks % C::BSTAGES) * C::B_BYTES;
+  };
+  auto copy_a = [&](uint32_t ks) {
     const uint8_t *abase = a.xq + uint64_t(ks) * C::BK;
-    const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
+    char *st = a_buf(ks);
 #pragma unroll
     for (uint32_t i = 0; i < C::A_COPIES; ++i) {
       dma16(abase + aoff[i], st + (i * C::WAVES + wave) * 1024);
     }
+  };
+  auto copy_b = [&](uint32_t ks) {
+    const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
+    char *st = b_buf(ks);
 #pragma unroll
     for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-      dma16(bbase + boff[i], st + C::A_BYTES + (i * C::WAVES + wave) * 1024);
+      dma16(bbase + boff[i], st + (i * C::WAVES + wave) * 1024);
     }
   };
+  constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
 
   f32x4 acc[C::TM][C::TN];
 #pragma unroll
@@ -239,17 +269,29 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     }
   }
 
-  stage(lds, 0);
+  copy_a(0);
+#pragma unroll
+  for (uint32_t b = 0; b < BAHEAD; ++b) {
+    if (b < ksteps) {
+      copy_b(b);
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   gemm_barrier();
 
   for (uint32_t ks = 0; ks < ksteps; ++ks) {
-    const char *cur = lds + (ks & 1) * C::STAGE;
+    // Issue order A(ks + 1) then B(ks + BAHEAD): the in-order vector-memory
+    // counter then proves A(ks + 1) (and every older B) landed while the
+    // newest B copies stay in flight.
     if (ks + 1 < ksteps) {
-      stage(lds + ((ks + 1) & 1) * C::STAGE, ks + 1);
+      copy_a(ks + 1);
     }
-    const char *As = cur + (wm * C::TM * 2) * 1024 + lane * 16;
-    const char *Bs = cur + C::A_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
+    const bool b_more = ks + BAHEAD < ksteps;
+    if (b_more) {
+      copy_b(ks + BAHEAD);
+    }
+    const char *As = a_buf(ks) + (wm * C::TM * 2) * 1024 + lane * 16;
+    const char *Bs = b_buf(ks) + (wn * C::TN * 2) * 1024 + lane * 16;
     i32x8 bf[C::TN];
 #pragma unroll
     for (uint32_t j = 0; j < C::TN; ++j) {
@@ -269,7 +311,11 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       af = an;
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the next stage's copies have landed
+    if (b_more && BAHEAD > 1) {
+      wait_vm<C::B_COPIES>();
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+    }
     gemm_barrier();
   }
 
@@ -355,7 +401,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   }
 }
 
-using GemmLarge = GemmCfg<256, 256, 2, 4>;  // default: 1 workgroup per CU
+using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 using GemmMid = GemmCfg<128, 128, 2, 2>;    // 2 workgroups per CU
 
 template <class C>
