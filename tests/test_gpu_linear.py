@@ -105,6 +105,32 @@ def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="aq4 gemv bf16")
 
 
+@pytest.mark.parametrize("m,n", [(1, 9000), (4, 25000), (8, 12500), (16, 12500)])
+@pytest.mark.parametrize("enc", ["fp8", "aq4"])
+def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
+    """Enough 16-row stripes (the last one ragged) that the launcher gives each
+    workgroup of the multi-stripe kernels a run of three or more stripes (at
+    M >= 4, on a 256-CU device); K = 4096 as in the Llama shapes."""
+    k = 4096
+    w = weights(n, k, tag=21)
+    xb = activations_bf16(orc, m, k, tag=m + 200)
+    if enc == "fp8":
+        q, s = orc.fp8_quantize_rows(w)
+        y_ref, _ = orc.fp8_gemv(xb, q, s)
+        lw = uh.LinearWeight.from_fp8(q, s)
+    else:
+        p, s, z = orc.aq4_quantize(w)
+        y_ref, _ = orc.aq4_gemv(xb, p, s, z)
+        lw = uh.LinearWeight.from_aq4(p, s, z)
+    x = to_torch_bf16(xb, gpu)
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} gemv f32 many stripes")
+    yb = lw.forward(x)
+    assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True,
+                 what=f"{enc} gemv bf16 many stripes")
+
+
 def test_gemv_strided_activation_and_alpha(uh, orc, gpu):
     n, k, m = 48, 384, 5
     w = weights(n, k, tag=9)

@@ -22,7 +22,8 @@
 // zero are applied once per 128 k in fp32.
 #include <cstdlib>
 #include <mutex>
-#include <unordered_set>
+#include <algorithm>
+#include <unordered_map>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -31,28 +32,38 @@ namespace ullm {
 namespace {
 
 // Activation row reader.  VEC: rows are 16-byte aligned and K covers every
-// unit, so each read is one unconditional 16-byte load; lanes whose row is past
-// M read row 0 and zero the value with a select, keeping the code free of
-// branches (a branch around a load forces the wait counter to drain).  The
-// scalar variant handles unaligned views and ragged K.
+// unit, so each read is one unconditional 16-byte buffer load.  The buffer
+// descriptor spans this workgroup's 32-row activation block; lanes whose row
+// is past M get an offset beyond the descriptor's range, which the hardware
+// answers with zeros without touching memory -- no branch (a branch around a
+// load forces the wait counter to drain) and no wasted traffic at small M.
+// The scalar variant handles unaligned views and ragged K.
 template <bool VEC>
 struct XRow {
   const uint16_t *row;
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t off;  // byte offset of this lane's row (VEC), out of range if m >= M
   bool valid;
   uint32_t K;
   XRow() = default;
   __device__ __forceinline__ XRow(const uint16_t *x, uint64_t ldx, uint32_t m,
                                   uint32_t M, uint32_t k)
-      : row(x + uint64_t(m < M ? m : 0) * ldx), valid(m < M), K(k) {}
+      : row(x + uint64_t(m < M ? m : 0) * ldx), valid(m < M), K(k) {
+    if constexpr (VEC) {
+      const uint32_t m0 = blockIdx.y * 32;
+      const uint32_t rows = min(M - m0, 32u);
+      const uint64_t extent = (uint64_t(rows - 1) * ldx + k) * 2;
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t *>(x + uint64_t(m0) * ldx), 0,
+          static_cast<int>(extent), 0x00020000);
+      off = valid ? uint32_t((m - m0) * ldx * 2) : 0x80000000u;
+    }
+  }
   __device__ __forceinline__ bf16x8 load8(uint32_t k0) const {
     u32x4 r;
     if constexpr (VEC) {
-      r = *reinterpret_cast<const u32x4 *>(row + k0);
-      const uint32_t keep = valid ? 0xffffffffu : 0u;
-      r.x &= keep;
-      r.y &= keep;
-      r.z &= keep;
-      r.w &= keep;
+      r = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + k0 * 2, 0, 0));
     } else {
       uint32_t h[8];
 #pragma unroll
@@ -66,9 +77,6 @@ struct XRow {
   }
 };
 
-// Sum the waves' partial tiles and store.  Thread o finishes outputs
-// (m, n = o % 16); `scale` is that column's row scale (1 for AQ4), loaded by
-// the caller at kernel start so no memory round trip sits in the epilogue.
 template <int MT, int WAVES>
 __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
                                                  f32x4 (&acc)[MT], float *red,
@@ -316,6 +324,10 @@ constexpr int kAq4LdsBatch = ULLM_AQ4_LDS_BATCH;
 #define ULLM_FP8_LDS_BATCH 4
 #endif
 constexpr int kFp8LdsBatch = ULLM_FP8_LDS_BATCH;
+#ifndef ULLM_AQ4_MS_BATCH
+#define ULLM_AQ4_MS_BATCH 4
+#endif
+constexpr int kAq4MsBatch = ULLM_AQ4_MS_BATCH;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -633,6 +645,204 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
   reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
 }
 
+// Cross-wave reduction of one stripe for the multi-stripe kernels: like
+// reduce_and_store, but for stripe T, through one of two LDS buffers that
+// alternate between stripes, and behind a barrier that leaves the weight
+// loads already issued for the next stripe in flight.
+template <int MT, int WAVES>
+__device__ __forceinline__ void flush_stripe(const GemvArgs &a,
+                                             f32x4 (&acc)[MT], float *red,
+                                             uint32_t T) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      red[((wave * MT + mt) * 4 + r) * kWave + lane] = acc[mt][r];
+    }
+  }
+  lds_barrier();
+  const uint32_t m_base = blockIdx.y * 32;
+  for (int o = threadIdx.x; o < MT * 256; o += WAVES * kWave) {
+    const int mt = o / 256;
+    const int mrow = (o % 256) / 16;
+    const int ncol = o % 16;
+    const int src_lane = ncol + 16 * (mrow / 4);
+    const int r = mrow % 4;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      v += red[((w * MT + mt) * 4 + r) * kWave + src_lane];
+    }
+    const uint32_t m = m_base + mt * 16 + mrow;
+    const uint32_t n = T * 16 + ncol;
+    if (m < a.m && n < a.n) {
+      v = a.alpha * v;
+      if (a.y_f32) {
+        static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
+      } else {
+        static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+// Multi-stripe AQ4 kernel.  A workgroup stages its activation block (and the
+// group sums) in LDS once and then walks a run of a.spw consecutive stripes,
+// its waves splitting K as in the single-stripe kernel.  The weight stream of
+// each wave is one continuous software pipeline across the stripes: the next
+// batch is in flight while the current one is contracted, including across
+// the per-stripe reduction, whose barrier does not wait on vector loads.
+// Staging x once per workgroup instead of once per stripe is what makes LDS
+// staging pay at M = 8..16, where x is as large as a stripe's weights.
+// Requires groups % (WAVES * B) == 0 (every wave's share is whole batches).
+template <int MT, int WAVES, int B>
+__global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
+    GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  __shared__ float red[2][WAVES * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t groups = a.units;
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t T0 = blockIdx.x * a.spw;
+  const uint32_t nS = min(a.spw, stripes - T0);
+  const uint32_t ub = groups * wave / WAVES;
+  const uint32_t ue = groups * (wave + 1) / WAVES;
+  const u32x4 *wbase = reinterpret_cast<const u32x4 *>(
+      static_cast<const uint32_t *>(a.tiles) + uint64_t(T0) * groups * 256 +
+      lane * 4);
+  const uint32_t *zbase = static_cast<const uint32_t *>(a.aux) +
+                          uint64_t(T0) * groups * 16 + lane % 16;
+  const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
+  const uint32_t cpr = a.k / 8;
+  float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * cpr * 8);
+
+  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  __builtin_amdgcn_sched_barrier(0);
+  // Tile g of stripe s sits at item s * groups + g of the run.
+  u32x4 cur[B];
+  uint32_t csz[B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    cur[i] = __builtin_nontemporal_load(wbase + uint64_t(ub + i) * 64);
+    csz[i] = zbase[uint64_t(ub + i) * 16];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<2 * B>();  // this thread's activation copies have landed
+  lds_barrier();
+  for (uint32_t base = 0; base < rows * groups * 16; base += WAVES * kWave) {
+    const uint32_t i = base + threadIdx.x;
+    const uint32_t item = i / 16, c = i % 16;
+    float sum = 0.0f;
+    if (item < rows * groups) {
+      const uint32_t r = item / groups, g = item % groups;
+      const u32x4 v =
+          *reinterpret_cast<const u32x4 *>(xs + x_slot(r, g * 16 + c, cpr) * 8);
+      sum = ((bits_f32(v.x << 16) + bits_f32(v.x & 0xffff0000u)) +
+             (bits_f32(v.y << 16) + bits_f32(v.y & 0xffff0000u))) +
+            ((bits_f32(v.z << 16) + bits_f32(v.z & 0xffff0000u)) +
+             (bits_f32(v.w << 16) + bits_f32(v.w & 0xffff0000u)));
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      sum += __shfl_xor(sum, off, kWave);
+    }
+    if (item < rows * groups && c == 0) {
+      gsum[item] = sum;
+    }
+  }
+  lds_barrier();
+
+  const uint32_t q4 = lane / 16;
+  const char *xa[MT][4];
+  const float *gs[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+    const uint32_t r = m < rows ? m : rows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xa[mt][j] = reinterpret_cast<const char *>(xs) +
+                  (r * cpr + ((q4 + 4 * j) ^ (r & 7u))) * 16;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t mr = mt * 16 + 4 * q4 + e;
+      gs[mt][e] = gsum + (mr < rows ? mr : 0) * groups;
+    }
+  }
+  const uint32_t nmask = opaque_u32(0x000f000fu);
+  const uint32_t nmagic = opaque_u32(0x43004300u);
+
+  for (uint32_t s = 0; s < nS; ++s) {
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (uint32_t g = ub; g < ue; g += B) {
+      // Next batch: the rest of this stripe, else the start of the next one.
+      const bool in_stripe = g + B < ue;
+      const bool more = in_stripe || s + 1 < nS;
+      const uint64_t nitem =
+          in_stripe ? uint64_t(s) * groups + g + B : uint64_t(s + 1) * groups + ub;
+      u32x4 nxt[B];
+      uint32_t nsz[B];
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          nxt[i] = __builtin_nontemporal_load(wbase + (nitem + i) * 64);
+          nsz[i] = zbase[(nitem + i) * 16];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 p[B][MT];
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          p[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const bf16x8 bj = nib8_to_bf16_off128(cur[i][j], nmask, nmagic);
+          const uint32_t off = (g + i) * 256;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            p[i][mt] = mfma_bf16(
+                *reinterpret_cast<const bf16x8 *>(xa[mt][j] + off), bj, p[i][mt]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const float sf = f16_to_f32(uint16_t(csz[i] & 0xffffu));
+        const float zoff = 128.0f + f16_to_f32(uint16_t(csz[i] >> 16));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][g + i]);
+          }
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          cur[i] = nxt[i];
+          csz[i] = nsz[i];
+        }
+      }
+    }
+    flush_stripe<MT, WAVES>(a, acc, red[s & 1], T0 + s);
+  }
+}
+
 // Waves per workgroup (they split K).  Measured on MI355X: FP8 streams best
 // with 8 waves per stripe at every Llama shape; AQ4 (half the bytes per
 // stripe) with 4 once the grid has enough stripes to fill the chip.
@@ -667,7 +877,7 @@ uint32_t lds_cap(bool aq4) {
     return e ? uint32_t(std::atoi(e)) * 1024u : 0u;
   }();
   const uint32_t cap = aq4 ? kXLdsBytesAq4 : kXLdsBytes;
-  return forced != 0 && forced < kXLdsBytes ? forced : cap;
+  return forced != 0 && forced <= kXLdsBytes ? forced : cap;
 }
 
 // Launch with `bytes` of dynamic LDS, raising the kernel's limit past the
@@ -676,17 +886,20 @@ template <typename Kernel>
 hipError_t launch_lds(Kernel kernel, dim3 grid, dim3 block, uint32_t bytes,
                       hipStream_t s, const GemvArgs &a) {
   if (bytes > 64 * 1024) {
+    // Raise the kernel's dynamic-LDS limit to what this launch needs (the
+    // limit plus the kernel's static LDS may not exceed the CU's 160 KiB).
     static std::mutex mu;
-    static std::unordered_set<const void *> raised;
+    static std::unordered_map<const void *, uint32_t> raised;
     std::lock_guard<std::mutex> lock(mu);
     const void *key = reinterpret_cast<const void *>(kernel);
-    if (raised.count(key) == 0) {
+    auto it = raised.find(key);
+    if (it == raised.end() || it->second < bytes) {
       const hipError_t e = hipFuncSetAttribute(
-          key, hipFuncAttributeMaxDynamicSharedMemorySize, int(kXLdsBytes));
+          key, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
       if (e != hipSuccess) {
         return e;
       }
-      raised.insert(key);
+      raised[key] = bytes;
     }
   }
   hipLaunchKernelGGL(kernel, grid, block, bytes, s, a);
@@ -719,6 +932,79 @@ hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+uint32_t cu_count() {
+  static std::mutex mu;
+  static std::unordered_map<int, uint32_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) {
+    return it->second;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+          hipSuccess || n <= 0) {
+    n = 256;
+  }
+  cache[dev] = uint32_t(n);
+  return uint32_t(n);
+}
+
+int env_int(const char *name, int dflt) {
+  const char *e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+
+// Multi-stripe kernels: enough workgroups for every CU to hold as many as its
+// LDS admits, each walking a run of consecutive stripes.
+constexpr int kMsWaves = 8;
+uint32_t ms_target(uint32_t lds) {
+  const uint32_t per_cu = std::max(
+      1u, std::min(160u * 1024u / (lds + 16u * 1024u), 32u / kMsWaves));
+  return cu_count() * per_cu;
+}
+
+// Whether the multi-stripe AQ4 kernel takes this launch.  It stages the
+// activation block once per workgroup and amortises it over a run of
+// stripes, which pays once the block is sizeable (M >= 4) and each workgroup
+// gets a run of 3 or more stripes.  Measured on MI355X, 4096 -> 28672 AQ4:
+// M=8 17.2 against 23.5 us, M=16 21.0 against 32.2 us, 4096 -> 128256 M=8
+// 58.5 against 89.5 us; at M = 1..2, and with runs of 1-2 stripes (4096 ->
+// 6144), the single-stripe kernels stay ahead.  ULLM_GEMV_MS=0/1 overrides.
+bool use_aq4_ms(const GemvArgs &a, bool vec, int mt) {
+  static const int forced = env_int("ULLM_GEMV_MS", -1);
+  if (!vec || !lds_allowed() || forced == 0) {
+    return false;
+  }
+  const uint32_t lds = lds_bytes(a, true);
+  // Dynamic (activation block) plus static (two reduction buffers) LDS must
+  // fit the CU's 160 KiB.
+  if (lds > kXLdsBytes || lds + 2u * kMsWaves * mt * 1024u > 160u * 1024u ||
+      a.units % (kMsWaves * kAq4MsBatch) != 0) {
+    return false;
+  }
+  if (forced == 1) {
+    return true;
+  }
+  const uint32_t stripes = a.n16 / 16;
+  return a.m >= 4 && stripes >= 3 * ms_target(lds);
+}
+
+template <typename Kernel>
+hipError_t launch_ms(Kernel kernel, GemvArgs a, hipStream_t s) {
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t target = ms_target(lds_bytes(a, true));
+  static const int forced = env_int("ULLM_GEMV_SPW", 0);
+  a.spw = forced > 0 ? uint32_t(forced) : (stripes + target - 1) / target;
+  const dim3 grid((stripes + a.spw - 1) / a.spw, (a.m + 31) / 32);
+  return launch_lds(kernel, grid, dim3(kMsWaves * kWave), lds_bytes(a, true),
+                    s, a);
+}
+
 template <int MT, int WAVES>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
@@ -742,8 +1028,11 @@ hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
 // Unconditional 16-byte activation reads need aligned rows and, for FP8, a
 // K that fills every 64-wide unit (AQ4 K is always a multiple of 128).
 bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
+  // The buffer descriptor of XRow<true> spans at most 32 rows; its byte
+  // extent must stay below 2^31 so that the out-of-range offset is rejected.
   return (reinterpret_cast<uintptr_t>(a.x) % 16 == 0) && (a.ldx % 8 == 0) &&
-         (a.k % unit_k == 0);
+         (a.k % unit_k == 0) &&
+         (uint64_t(31) * a.ldx + a.k) * 2 < (uint64_t(1) << 31);
 }
 
 }  // namespace
@@ -766,8 +1055,12 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
 
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
-  const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
+  if (use_aq4_ms(a, vec, two ? 2 : 1)) {
+    return two ? launch_ms(aq4_gemv_ms_kernel<2, kMsWaves, kAq4MsBatch>, a, s)
+               : launch_ms(aq4_gemv_ms_kernel<1, kMsWaves, kAq4MsBatch>, a, s);
+  }
+  const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
     case 4: return launch_aq4_t<1, 2>(a, vec, s);
     case 5: return launch_aq4_t<2, 2>(a, vec, s);

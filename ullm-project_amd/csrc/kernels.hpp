@@ -49,6 +49,7 @@ struct GemvArgs {
   uint32_t units;      // FP8: k64 / 64; AQ4: k / 128
   float alpha;
   bool y_f32;
+  uint32_t spw;        // stripes per workgroup (multi-stripe kernels; set by the launcher)
 };
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s);
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s);
