@@ -324,10 +324,6 @@ constexpr int kAq4LdsBatch = ULLM_AQ4_LDS_BATCH;
 #define ULLM_FP8_LDS_BATCH 4
 #endif
 constexpr int kFp8LdsBatch = ULLM_FP8_LDS_BATCH;
-#ifndef ULLM_AQ4_MS_BATCH
-#define ULLM_AQ4_MS_BATCH 4
-#endif
-constexpr int kAq4MsBatch = ULLM_AQ4_MS_BATCH;
 
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
@@ -652,7 +648,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
 template <int MT, int WAVES>
 __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
                                              f32x4 (&acc)[MT], float *red,
-                                             uint32_t T) {
+                                             uint32_t T, float scale) {
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
 #pragma unroll
@@ -678,7 +674,7 @@ __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
     const uint32_t m = m_base + mt * 16 + mrow;
     const uint32_t n = T * 16 + ncol;
     if (m < a.m && n < a.n) {
-      v = a.alpha * v;
+      v = a.alpha * (scale * v);
       if (a.y_f32) {
         static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
       } else {
@@ -688,49 +684,89 @@ __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
   }
 }
 
+// Byte-range buffer over device memory for the multi-stripe kernels: loads at
+// offsets past `bytes` return zero without a memory access, which lets the
+// software pipeline issue its look-ahead loads unconditionally (a branch
+// around a load makes the compiler drain every outstanding load at the join).
+// Offsets are 32-bit: a run must stay below 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *p,
+                                                             uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+constexpr int kNt = 2;                      // nontemporal cache policy bit
+
 // Multi-stripe AQ4 kernel.  A workgroup stages its activation block (and the
 // group sums) in LDS once and then walks a run of a.spw consecutive stripes,
-// its waves splitting K as in the single-stripe kernel.  The weight stream of
-// each wave is one continuous software pipeline across the stripes: the next
-// batch is in flight while the current one is contracted, including across
-// the per-stripe reduction, whose barrier does not wait on vector loads.
-// Staging x once per workgroup instead of once per stripe is what makes LDS
-// staging pay at M = 8..16, where x is as large as a stripe's weights.
+// its waves splitting K as in the single-stripe kernel.  Each wave's weight
+// stream is one software pipeline over the whole run: two register buffers
+// alternate, so batch t + 1 is in flight while batch t is contracted, also
+// across the per-stripe reduction (whose barrier waits on LDS only).  Loop
+// bounds are wave-uniform scalars and the look-ahead loads are unconditional
+// (past the run they read zeros from outside the buffer range), so no wait
+// on outstanding loads is forced before the data is used.  Staging x once per
+// workgroup instead of once per stripe is what makes LDS staging pay at
+// M = 4..16, where x is as large as a stripe's weights.
 // Requires groups % (WAVES * B) == 0 (every wave's share is whole batches).
-template <int MT, int WAVES, int B>
+template <int MT, int WAVES, int B, int DEPTH>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
   __shared__ float red[2][WAVES * MT * 4 * kWave];
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t groups = a.units;
   const uint32_t stripes = a.n16 / 16;
   const uint32_t T0 = blockIdx.x * a.spw;
   const uint32_t nS = min(a.spw, stripes - T0);
   const uint32_t ub = groups * wave / WAVES;
   const uint32_t ue = groups * (wave + 1) / WAVES;
-  const u32x4 *wbase = reinterpret_cast<const u32x4 *>(
-      static_cast<const uint32_t *>(a.tiles) + uint64_t(T0) * groups * 256 +
-      lane * 4);
-  const uint32_t *zbase = static_cast<const uint32_t *>(a.aux) +
-                          uint64_t(T0) * groups * 16 + lane % 16;
+  const uint32_t nbw = (ue - ub) / B;  // batches per stripe
+  const uint32_t NB = nS * nbw;        // batches of the run
+  const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
+      static_cast<const uint8_t *>(a.tiles) + uint64_t(T0) * groups * 1024,
+      nS * groups * 1024);
+  const __amdgpu_buffer_rsrc_t zbuf = byte_buffer(
+      static_cast<const uint32_t *>(a.aux) + uint64_t(T0) * groups * 16,
+      nS * groups * 64);
   const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
   const uint32_t cpr = a.k / 8;
   float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * cpr * 8);
 
+  struct Batch {
+    u32x4 w[B];
+    uint32_t sz[B];
+  };
+  // Load pointer: stripe ls, group lg of the run (scalars).  Past the last
+  // batch it runs on into stripe nS and beyond, outside both buffers, so the
+  // look-ahead loads there read zeros and touch no memory.
+  uint32_t ls = 0, lg = ub;
+  auto issue = [&](Batch &bt) {
+    const uint32_t item = ls * groups + lg;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      bt.w[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     wbuf, (item + i) * 1024 + lane * 16, 0, kNt));
+      bt.sz[i] = __builtin_amdgcn_raw_buffer_load_b32(
+          zbuf, (item + i) * 64 + (lane % 16) * 4, 0, 0);
+    }
+    lg += B;
+    if (lg == ue) {
+      lg = ub;
+      ++ls;
+    }
+  };
+
   stage_x_lds<WAVES>(a, xs, rows, cpr);
   __builtin_amdgcn_sched_barrier(0);
-  // Tile g of stripe s sits at item s * groups + g of the run.
-  u32x4 cur[B];
-  uint32_t csz[B];
+  Batch ring[DEPTH];
 #pragma unroll
-  for (int i = 0; i < B; ++i) {
-    cur[i] = __builtin_nontemporal_load(wbase + uint64_t(ub + i) * 64);
-    csz[i] = zbase[uint64_t(ub + i) * 16];
+  for (int r = 0; r + 1 < DEPTH; ++r) {
+    issue(ring[r]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<2 * B>();  // this thread's activation copies have landed
+  wait_vmcnt<(DEPTH - 1) * (2 * B)>();  // this thread's activation copies have landed
   lds_barrier();
   for (uint32_t base = 0; base < rows * groups * 16; base += WAVES * kWave) {
     const uint32_t i = base + threadIdx.x;
@@ -776,70 +812,210 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   const uint32_t nmask = opaque_u32(0x000f000fu);
   const uint32_t nmagic = opaque_u32(0x43004300u);
 
-  for (uint32_t s = 0; s < nS; ++s) {
-    f32x4 acc[MT];
+  f32x4 acc[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt) {
+    acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  // Consume pointer: stripe cs, group cg.
+  uint32_t cs = 0, cg = ub;
+  auto consume = [&](const Batch &bt) {
+    f32x4 p[B][MT];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        p[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
     }
-    for (uint32_t g = ub; g < ue; g += B) {
-      // Next batch: the rest of this stripe, else the start of the next one.
-      const bool in_stripe = g + B < ue;
-      const bool more = in_stripe || s + 1 < nS;
-      const uint64_t nitem =
-          in_stripe ? uint64_t(s) * groups + g + B : uint64_t(s + 1) * groups + ub;
-      u32x4 nxt[B];
-      uint32_t nsz[B];
-      if (more) {
+    // Independent MFMA chains interleaved (j outer, group inner).
 #pragma unroll
-        for (int i = 0; i < B; ++i) {
-          nxt[i] = __builtin_nontemporal_load(wbase + (nitem + i) * 64);
-          nsz[i] = zbase[(nitem + i) * 16];
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][j], nmask, nmagic);
+        const uint32_t off = (cg + i) * 256;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          p[i][mt] = mfma_bf16(
+              *reinterpret_cast<const bf16x8 *>(xa[mt][j] + off), bj, p[i][mt]);
         }
       }
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const float sf = f16_to_f32(uint16_t(bt.sz[i] & 0xffffu));
+      const float zoff = 128.0f + f16_to_f32(uint16_t(bt.sz[i] >> 16));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][cg + i]);
+        }
+      }
+    }
+    cg += B;
+    if (cg == ue) {  // stripe done: reduce across waves, store, reset
+      flush_stripe<MT, WAVES>(a, acc, red[cs & 1], T0 + cs, 1.0f);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      cg = ub;
+      ++cs;
+    }
+  };
+
+  // Ring of DEPTH batch buffers: DEPTH - 1 batches stay in flight while
+  // one is contracted.  Indices are compile-time, so the ring lives in
+  // registers.
+  for (uint32_t t = 0; t < NB; t += DEPTH) {
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+      issue(ring[(r + DEPTH - 1) % DEPTH]);
       __builtin_amdgcn_sched_barrier(0);
-      f32x4 p[B][MT];
-#pragma unroll
-      for (int i = 0; i < B; ++i) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          p[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-          const bf16x8 bj = nib8_to_bf16_off128(cur[i][j], nmask, nmagic);
-          const uint32_t off = (g + i) * 256;
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            p[i][mt] = mfma_bf16(
-                *reinterpret_cast<const bf16x8 *>(xa[mt][j] + off), bj, p[i][mt]);
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < B; ++i) {
-        const float sf = f16_to_f32(uint16_t(csz[i] & 0xffffu));
-        const float zoff = 128.0f + f16_to_f32(uint16_t(csz[i] >> 16));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][g + i]);
-          }
-        }
-      }
-      if (more) {
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-          cur[i] = nxt[i];
-          csz[i] = nsz[i];
-        }
+      if (t + r < NB) {
+        consume(ring[r]);
       }
     }
-    flush_stripe<MT, WAVES>(a, acc, red[s & 1], T0 + s);
+  }
+}
+
+// Multi-stripe FP8 kernel: the AQ4 multi-stripe kernel's structure (x staged
+// once per workgroup, a run of a.spw stripes, one ping-pong software pipeline
+// per wave over the run) with 64-k FP8 units.  Each batch also carries the
+// row scales of its stripe, applied once in the per-stripe reduction.
+// Requires units % (WAVES * B) == 0.
+template <int MT, int WAVES, int B, int DEPTH>
+__global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
+    GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
+  __shared__ float red[2][WAVES * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t units = a.units;
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t T0 = blockIdx.x * a.spw;
+  const uint32_t nS = min(a.spw, stripes - T0);
+  const uint32_t ub = units * wave / WAVES;
+  const uint32_t ue = units * (wave + 1) / WAVES;
+  const uint32_t nbw = (ue - ub) / B;
+  const uint32_t NB = nS * nbw;
+  const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
+      static_cast<const uint8_t *>(a.tiles) + uint64_t(T0) * units * 1024,
+      nS * units * 1024);
+  const __amdgpu_buffer_rsrc_t sbuf = byte_buffer(
+      static_cast<const float *>(a.aux) + uint64_t(T0) * 16, nS * 64);
+  const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
+  const uint32_t cpr = a.k / 8;
+
+  struct Batch {
+    u32x4 w[B];
+    float rs;  // row scale of the batch's stripe (column lane % 16)
+  };
+  uint32_t ls = 0, lu = ub;
+  auto issue = [&](Batch &bt) {
+    const uint32_t item = ls * units + lu;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      bt.w[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     wbuf, (item + i) * 1024 + lane * 16, 0, kNt));
+    }
+    bt.rs = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(
+                   sbuf, (ls * 16 + lane % 16) * 4, 0, 0));
+    lu += B;
+    if (lu == ue) {
+      lu = ub;
+      ++ls;
+    }
+  };
+
+  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  __builtin_amdgcn_sched_barrier(0);
+  Batch ring[DEPTH];
+#pragma unroll
+  for (int r = 0; r + 1 < DEPTH; ++r) {
+    issue(ring[r]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<(DEPTH - 1) * (B + 1)>();  // this thread's activation copies have landed
+  lds_barrier();
+
+  const uint32_t cgk = 2 * (lane / 16);
+  const char *xa[MT][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+    const uint32_t r = m < rows ? m : rows;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      xa[mt][h] = reinterpret_cast<const char *>(xs) +
+                  (r * cpr + ((cgk + h) ^ (r & 7u))) * 16;
+    }
+  }
+  f32x4 acc4[4][MT];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc4[c][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  zero_acc();
+  uint32_t cs = 0, cu = ub;
+  auto consume = [&](const Batch &bt) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const u32x4 wv = bt.w[i];
+      const u32x2 b01 = e4m3x4_to_bf16x4(wv.x);
+      const u32x2 b23 = e4m3x4_to_bf16x4(wv.y);
+      const u32x2 b45 = e4m3x4_to_bf16x4(wv.z);
+      const u32x2 b67 = e4m3x4_to_bf16x4(wv.w);
+      const bf16x8 w0 =
+          __builtin_bit_cast(bf16x8, u32x4{b01.x, b01.y, b23.x, b23.y});
+      const bf16x8 w1 =
+          __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
+      const uint32_t off = (cu + i) * 128;
+      const int ca = 2 * (i & 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc4[ca][mt] = mfma_bf16(
+            *reinterpret_cast<const bf16x8 *>(xa[mt][0] + off), w0, acc4[ca][mt]);
+        acc4[ca + 1][mt] = mfma_bf16(
+            *reinterpret_cast<const bf16x8 *>(xa[mt][1] + off), w1,
+            acc4[ca + 1][mt]);
+      }
+    }
+    cu += B;
+    if (cu == ue) {
+      f32x4 acc[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt] = (acc4[0][mt] + acc4[1][mt]) + (acc4[2][mt] + acc4[3][mt]);
+      }
+      flush_stripe<MT, WAVES>(a, acc, red[cs & 1], T0 + cs, bt.rs);
+      zero_acc();
+      cu = ub;
+      ++cs;
+    }
+  };
+
+  // Ring of DEPTH batch buffers: DEPTH - 1 batches stay in flight while
+  // one is contracted.  Indices are compile-time, so the ring lives in
+  // registers.
+  for (uint32_t t = 0; t < NB; t += DEPTH) {
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+      issue(ring[(r + DEPTH - 1) % DEPTH]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + r < NB) {
+        consume(ring[r]);
+      }
+    }
   }
 }
 
@@ -959,50 +1135,111 @@ int env_int(const char *name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
-// Multi-stripe kernels: enough workgroups for every CU to hold as many as its
-// LDS admits, each walking a run of consecutive stripes.
-constexpr int kMsWaves = 8;
-uint32_t ms_target(uint32_t lds) {
-  const uint32_t per_cu = std::max(
-      1u, std::min(160u * 1024u / (lds + 16u * 1024u), 32u / kMsWaves));
-  return cu_count() * per_cu;
+// Multi-stripe kernels: as many workgroups as the device holds at once (by
+// the occupancy calculator: registers and LDS), each walking a run of
+// consecutive stripes.
+template <typename Kernel>
+uint32_t resident_blocks(Kernel kernel, uint32_t threads, uint32_t lds) {
+  static std::mutex mu;
+  static std::unordered_map<uint64_t, uint32_t> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const uint64_t key = (uint64_t(reinterpret_cast<uintptr_t>(
+                            reinterpret_cast<const void *>(kernel))) << 8) ^
+                       (uint64_t(lds) << 20) ^ uint64_t(dev);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) {
+    return it->second;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu, reinterpret_cast<const void *>(kernel), int(threads),
+          size_t(lds)) != hipSuccess || per_cu < 1) {
+    per_cu = 1;
+  }
+  const uint32_t n = cu_count() * uint32_t(per_cu);
+  cache[key] = n;
+  return n;
 }
 
-// Whether the multi-stripe AQ4 kernel takes this launch.  It stages the
+// Multi-stripe kernel configurations (waves, units per batch, ring depth),
+// chosen by measurement on MI355X; overridable at build time for tuning.
+#ifndef ULLM_AQ4_MS_CFG
+#define ULLM_AQ4_MS_CFG 8, 2, 2
+#endif
+#ifndef ULLM_FP8_MS_CFG
+#define ULLM_FP8_MS_CFG 8, 4, 2
+#endif
+struct MsCfg {
+  int waves, batch, depth;
+};
+constexpr MsCfg kAq4Ms{ULLM_AQ4_MS_CFG};
+constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
+
+// Whether the multi-stripe kernel takes this launch.  It stages the
 // activation block once per workgroup and amortises it over a run of
-// stripes, which pays once the block is sizeable (M >= 4) and each workgroup
-// gets a run of 3 or more stripes.  Measured on MI355X, 4096 -> 28672 AQ4:
-// M=8 17.2 against 23.5 us, M=16 21.0 against 32.2 us, 4096 -> 128256 M=8
-// 58.5 against 89.5 us; at M = 1..2, and with runs of 1-2 stripes (4096 ->
-// 6144), the single-stripe kernels stay ahead.  ULLM_GEMV_MS=0/1 overrides.
-bool use_aq4_ms(const GemvArgs &a, bool vec, int mt) {
+// stripes.  Measured on MI355X (AQ4, K = 4096, 8 waves, batches of 2
+// groups): M=1 4096->14336 8.2 against 8.6 us for the single-stripe kernel,
+// M=8 4096->28672 15.9 against 23.0 us, M=8 4096->128256 51.3 against 89.0
+// us; but at M >= 4 a run of under 3 stripes per workgroup (4096->6144 at
+// M=8) loses to the register kernel, which reads only its share of x.
+// ULLM_GEMV_MS=0/1 overrides the choice.
+bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   static const int forced = env_int("ULLM_GEMV_MS", -1);
+  const MsCfg c = aq4 ? kAq4Ms : kFp8Ms;
   if (!vec || !lds_allowed() || forced == 0) {
     return false;
   }
-  const uint32_t lds = lds_bytes(a, true);
+  const uint32_t lds = lds_bytes(a, aq4);
+  const uint32_t stripes = a.n16 / 16;
   // Dynamic (activation block) plus static (two reduction buffers) LDS must
-  // fit the CU's 160 KiB.
-  if (lds > kXLdsBytes || lds + 2u * kMsWaves * mt * 1024u > 160u * 1024u ||
-      a.units % (kMsWaves * kAq4MsBatch) != 0) {
+  // fit the CU's 160 KiB; a run's weights must stay below 2 GiB (32-bit
+  // buffer offsets; checked for the whole matrix, the longest possible run).
+  if (lds > kXLdsBytes || lds + 2u * c.waves * mt * 1024u > 160u * 1024u ||
+      a.units % uint32_t(c.waves * c.batch) != 0 ||
+      uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31)) {
     return false;
   }
   if (forced == 1) {
     return true;
   }
-  const uint32_t stripes = a.n16 / 16;
-  return a.m >= 4 && stripes >= 3 * ms_target(lds);
+  // FP8 (measured, 8 waves, batches of 4 units): M=8 4096->28672 20.6
+  // against 25.1 us, M=16 21.9 against 39.4 us, M=8 4096->6144 7.1 against
+  // 7.9 us; at M = 1..4 the single-stripe kernel is level or ahead on the
+  // larger shapes (M=1 4096->28672 20.2 against 21.5 us).
+  if (!aq4) {
+    return a.m >= 8;
+  }
+  // AQ4: runs of 3+ stripes at M >= 4, taking two resident workgroups per CU
+  // when the activation block leaves room for two.
+  const uint32_t per_cu = lds + 16u * 1024u <= 80u * 1024u ? 2u : 1u;
+  return a.m <= 2 || stripes >= 3 * cu_count() * per_cu;
 }
 
 template <typename Kernel>
-hipError_t launch_ms(Kernel kernel, GemvArgs a, hipStream_t s) {
+hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
+                     hipStream_t s) {
   const uint32_t stripes = a.n16 / 16;
-  const uint32_t target = ms_target(lds_bytes(a, true));
+  const uint32_t target = resident_blocks(kernel, waves * kWave, lds);
   static const int forced = env_int("ULLM_GEMV_SPW", 0);
   a.spw = forced > 0 ? uint32_t(forced) : (stripes + target - 1) / target;
   const dim3 grid((stripes + a.spw - 1) / a.spw, (a.m + 31) / 32);
-  return launch_lds(kernel, grid, dim3(kMsWaves * kWave), lds_bytes(a, true),
-                    s, a);
+  return launch_lds(kernel, grid, dim3(waves * kWave), lds, s, a);
+}
+
+template <int MT>
+hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
+  return launch_ms(
+      aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.batch, kAq4Ms.depth>, a,
+      kAq4Ms.waves, lds_bytes(a, true), s);
+}
+
+template <int MT>
+hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
+  return launch_ms(
+      fp8_gemv_ms_kernel<MT, kFp8Ms.waves, kFp8Ms.batch, kFp8Ms.depth>, a,
+      kFp8Ms.waves, lds_bytes(a, false), s);
 }
 
 template <int MT, int WAVES>
@@ -1039,8 +1276,11 @@ bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
 
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 64);
-  const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   const bool two = a.m > 16;
+  if (use_ms(a, vec, two ? 2 : 1, false)) {
+    return two ? launch_fp8_ms<2>(a, s) : launch_fp8_ms<1>(a, s);
+  }
+  const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
     case 4: return launch_fp8_t<1, 2>(a, vec, s);
     case 5: return launch_fp8_t<2, 2>(a, vec, s);
@@ -1056,9 +1296,8 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
-  if (use_aq4_ms(a, vec, two ? 2 : 1)) {
-    return two ? launch_ms(aq4_gemv_ms_kernel<2, kMsWaves, kAq4MsBatch>, a, s)
-               : launch_ms(aq4_gemv_ms_kernel<1, kMsWaves, kAq4MsBatch>, a, s);
+  if (use_ms(a, vec, two ? 2 : 1, true)) {
+    return two ? launch_aq4_ms<2>(a, s) : launch_aq4_ms<1>(a, s);
   }
   const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
