@@ -696,60 +696,164 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *p,
 }
 constexpr int kNt = 2;                      // nontemporal cache policy bit
 
+// Activation block layout of the multi-stripe kernels: row r's 16-byte
+// chunk c at slot r * (cpr + 1) + c.  The one-chunk row padding puts the 16
+// rows an MFMA A read touches (same chunk, consecutive rows) in 16 different
+// bank groups, and every chunk of a lane sits at a fixed offset from the
+// lane's row base, so A reads need no per-read address arithmetic.  Row
+// `rows` is all zero; lanes whose row is past M read it.
+template <int WAVES>
+__device__ __forceinline__ void stage_x_pad(const GemvArgs &a, uint16_t *xs,
+                                            uint32_t rows, uint32_t cpr) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t pitch = cpr + 1;
+  const uint32_t total = rows * pitch;
+  const uint32_t m0 = blockIdx.y * 32;
+  for (uint32_t base = wave * kWave; base < total; base += WAVES * kWave) {
+    const uint32_t p = base + lane;
+    const uint32_t r = p / pitch, c = p % pitch;
+    if (p < total && c < cpr) {
+      const uint16_t *src = a.x + uint64_t(m0 + r) * a.ldx + c * 8;
+      __builtin_amdgcn_global_load_lds(
+          (__attribute__((address_space(1))) void *)(src),
+          (__attribute__((address_space(3))) void *)(xs + base * 8), 16, 0, 0);
+    }
+  }
+  for (uint32_t c = threadIdx.x; c < cpr; c += WAVES * kWave) {
+    *reinterpret_cast<u32x4 *>(xs + (total + c) * 8) = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// LDS bytes of the multi-stripe kernels: padded activation rows, the zero
+// row, and (AQ4) the per-(row, group) sums.
+uint32_t ms_lds_bytes(const GemvArgs &a, bool aq4) {
+  const uint32_t rows = min(a.m, 32u);
+  return (rows + 1) * (a.k * 2 + 16) + (aq4 ? rows * (a.k / 128) * 4 : 0);
+}
+
+// End of one stripe for the multi-stripe kernels, for the KS waves that
+// split its K: with KS = 1 each lane stores its accumulators directly (lane
+// l holds rows 4 (l / 16) + r, column l % 16 of every 16 x 16 tile); with
+// KS > 1 the partial sums meet in LDS behind a workgroup barrier that does
+// not wait on vector loads (the next stripe's weights stay in flight), and
+// the sub-group's threads store.  `red` is this sub-group's buffer, `kw` the
+// wave's index within it, `live` whether the stripe exists.
+template <int MT, int KS>
+__device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
+                                         float *red, uint32_t T, float scale,
+                                         uint32_t kw, bool live) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t m_base = blockIdx.y * 32;
+  auto store = [&](uint32_t m, uint32_t n, float v) {
+    if (live && m < a.m && n < a.n) {
+      v = a.alpha * (scale * v);
+      if (a.y_f32) {
+        static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
+      } else {
+        static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
+      }
+    }
+  };
+  if constexpr (KS == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        store(m_base + mt * 16 + 4 * (lane / 16) + r, T * 16 + lane % 16,
+              acc[mt][r]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        red[((kw * MT + mt) * 4 + r) * kWave + lane] = acc[mt][r];
+      }
+    }
+    lds_barrier();
+    for (uint32_t o = kw * kWave + lane; o < MT * 256; o += KS * kWave) {
+      const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
+      const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < KS; ++w) {
+        v += red[((w * MT + mt) * 4 + r) * kWave + src];
+      }
+      store(m_base + mt * 16 + mrow, T * 16 + ncol, v);
+    }
+  }
+}
+
 // Multi-stripe AQ4 kernel.  A workgroup stages its activation block (and the
-// group sums) in LDS once and then walks a run of a.spw consecutive stripes,
-// its waves splitting K as in the single-stripe kernel.  Each wave's weight
-// stream is one software pipeline over the whole run: two register buffers
-// alternate, so batch t + 1 is in flight while batch t is contracted, also
-// across the per-stripe reduction (whose barrier waits on LDS only).  Loop
-// bounds are wave-uniform scalars and the look-ahead loads are unconditional
-// (past the run they read zeros from outside the buffer range), so no wait
-// on outstanding loads is forced before the data is used.  Staging x once per
-// workgroup instead of once per stripe is what makes LDS staging pay at
-// M = 4..16, where x is as large as a stripe's weights.
-// Requires groups % (WAVES * B) == 0 (every wave's share is whole batches).
-template <int MT, int WAVES, int B, int DEPTH>
+// group sums) in LDS once and then works through a run of a.spw consecutive
+// stripes.  Its WAVES waves form WAVES / KS sub-groups; sub-group g takes
+// stripes g, g + WAVES / KS, ... of the run, and its KS waves split each
+// stripe's K (KS = 1: a wave owns whole stripes and needs no reduction).
+// Each wave's weight stream is one software pipeline over all its stripes: a
+// ring of DEPTH batch buffers keeps DEPTH - 1 batches in flight while one is
+// contracted, also across the per-stripe reduction.  Loop bounds are
+// wave-uniform scalars and look-ahead loads are unconditional (past the run,
+// or for a sub-group's missing last stripe, they read zeros from outside the
+// buffer range without touching memory), so no wait on outstanding loads is
+// forced before the data is used; the tile offset is a scalar operand of the
+// buffer load.  Staging x once per workgroup instead of once per stripe is
+// what makes LDS staging pay at M = 4..16, where x is as large as a stripe's
+// weights.
+// NR: accumulator elements that can hold a valid row (M <= 4 leaves rows
+// 4..15 of the 16-row MFMA tile empty, so only elements r < NR carry results
+// and need the per-group correction).
+// Requires groups % (KS * B) == 0 (every wave's share is whole batches).
+template <int MT, int WAVES, int KS, int B, int DEPTH, int NR>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     GemvArgs a) {
+  static_assert(NR == 4 || MT == 1, "NR < 4 only for a single m-tile");
+  static_assert(WAVES % KS == 0, "sub-groups");
+  constexpr uint32_t SG = WAVES / KS;
+  constexpr uint32_t RED = KS > 1 ? 2 * WAVES * MT * 4 * kWave : 1;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
-  __shared__ float red[2][WAVES * MT * 4 * kWave];
+  __shared__ float red[RED];
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t sg = wave / KS, kw = wave % KS;
   const uint32_t groups = a.units;
   const uint32_t stripes = a.n16 / 16;
   const uint32_t T0 = blockIdx.x * a.spw;
   const uint32_t nS = min(a.spw, stripes - T0);
-  const uint32_t ub = groups * wave / WAVES;
-  const uint32_t ue = groups * (wave + 1) / WAVES;
+  const uint32_t per_sg = (nS + SG - 1) / SG;  // stripes per sub-group (uniform)
+  const uint32_t ub = groups * kw / KS;
+  const uint32_t ue = groups * (kw + 1) / KS;
   const uint32_t nbw = (ue - ub) / B;  // batches per stripe
-  const uint32_t NB = nS * nbw;        // batches of the run
+  const uint32_t NB = per_sg * nbw;    // batches of this wave
   const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
       static_cast<const uint8_t *>(a.tiles) + uint64_t(T0) * groups * 1024,
       nS * groups * 1024);
   const __amdgpu_buffer_rsrc_t zbuf = byte_buffer(
       static_cast<const uint32_t *>(a.aux) + uint64_t(T0) * groups * 16,
       nS * groups * 64);
+  const uint32_t wlane = lane * 16, zlane = (lane % 16) * 4;
   const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
   const uint32_t cpr = a.k / 8;
-  float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * cpr * 8);
+  const uint32_t pitch = cpr + 1;
+  float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * pitch * 8);
 
   struct Batch {
     u32x4 w[B];
     uint32_t sz[B];
   };
-  // Load pointer: stripe ls, group lg of the run (scalars).  Past the last
-  // batch it runs on into stripe nS and beyond, outside both buffers, so the
-  // look-ahead loads there read zeros and touch no memory.
+  // Load pointer: the wave's ls-th stripe (run stripe sg + ls * SG), group
+  // lg (scalars).
   uint32_t ls = 0, lg = ub;
   auto issue = [&](Batch &bt) {
-    const uint32_t item = ls * groups + lg;
+    const uint32_t item = (sg + ls * SG) * groups + lg;
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       bt.w[i] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     wbuf, (item + i) * 1024 + lane * 16, 0, kNt));
-      bt.sz[i] = __builtin_amdgcn_raw_buffer_load_b32(
-          zbuf, (item + i) * 64 + (lane % 16) * 4, 0, 0);
+                     wbuf, wlane, (item + i) * 1024, kNt));
+      bt.sz[i] = __builtin_amdgcn_raw_buffer_load_b32(zbuf, zlane,
+                                                      (item + i) * 64, 0);
     }
     lg += B;
     if (lg == ue) {
@@ -758,7 +862,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     }
   };
 
-  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  stage_x_pad<WAVES>(a, xs, rows, cpr);
   __builtin_amdgcn_sched_barrier(0);
   Batch ring[DEPTH];
 #pragma unroll
@@ -766,16 +870,17 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     issue(ring[r]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<(DEPTH - 1) * (2 * B)>();  // this thread's activation copies have landed
+  wait_vmcnt<(DEPTH - 1) * 2 * B>();  // this thread's activation copies landed
   lds_barrier();
+  // Group sums: 16 lanes per (row, group), one chunk each, then a butterfly.
   for (uint32_t base = 0; base < rows * groups * 16; base += WAVES * kWave) {
     const uint32_t i = base + threadIdx.x;
     const uint32_t item = i / 16, c = i % 16;
     float sum = 0.0f;
     if (item < rows * groups) {
       const uint32_t r = item / groups, g = item % groups;
-      const u32x4 v =
-          *reinterpret_cast<const u32x4 *>(xs + x_slot(r, g * 16 + c, cpr) * 8);
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(
+          xs + (r * pitch + g * 16 + c) * 8);
       sum = ((bits_f32(v.x << 16) + bits_f32(v.x & 0xffff0000u)) +
              (bits_f32(v.y << 16) + bits_f32(v.y & 0xffff0000u))) +
             ((bits_f32(v.z << 16) + bits_f32(v.z & 0xffff0000u)) +
@@ -791,21 +896,18 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   }
   lds_barrier();
 
-  const uint32_t q4 = lane / 16;
-  const char *xa[MT][4];
-  const float *gs[MT][4];
+  // A operand of group g, MFMA j: chunk 16 g + 4 j + lane / 16 of the lane's
+  // row, i.e. byte (16 g + 4 j) * 16 past the lane base.
+  const char *xa[MT];
+  const float *gs[MT][4];  // group-sum row of each accumulator element
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const uint32_t m = mt * 16 + lane % 16;
     const uint32_t r = m < rows ? m : rows;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      xa[mt][j] = reinterpret_cast<const char *>(xs) +
-                  (r * cpr + ((q4 + 4 * j) ^ (r & 7u))) * 16;
-    }
+    xa[mt] = reinterpret_cast<const char *>(xs) + (r * pitch + lane / 16) * 16;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint32_t mr = mt * 16 + 4 * q4 + e;
+      const uint32_t mr = mt * 16 + 4 * (lane / 16) + e;
       gs[mt][e] = gsum + (mr < rows ? mr : 0) * groups;
     }
   }
@@ -817,7 +919,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   for (int mt = 0; mt < MT; ++mt) {
     acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  // Consume pointer: stripe cs, group cg.
+  // Consume pointer: the wave's cs-th stripe, group cg.
   uint32_t cs = 0, cg = ub;
   auto consume = [&](const Batch &bt) {
     f32x4 p[B][MT];
@@ -834,11 +936,11 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
 #pragma unroll
       for (int i = 0; i < B; ++i) {
         const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][j], nmask, nmagic);
-        const uint32_t off = (cg + i) * 256;
+        const uint32_t off = ((cg + i) * 16 + 4 * j) * 16;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           p[i][mt] = mfma_bf16(
-              *reinterpret_cast<const bf16x8 *>(xa[mt][j] + off), bj, p[i][mt]);
+              *reinterpret_cast<const bf16x8 *>(xa[mt] + off), bj, p[i][mt]);
         }
       }
     }
@@ -849,14 +951,16 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < NR; ++r) {
           acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][cg + i]);
         }
       }
     }
     cg += B;
-    if (cg == ue) {  // stripe done: reduce across waves, store, reset
-      flush_stripe<MT, WAVES>(a, acc, red[cs & 1], T0 + cs, 1.0f);
+    if (cg == ue) {  // stripe done: reduce, store, reset
+      const uint32_t sr = sg + cs * SG;  // run stripe
+      flush_ks<MT, KS>(a, acc, red + (cs & 1) * (RED / 2) + sg * KS * MT * 4 * kWave,
+                       T0 + sr, 1.0f, kw, sr < nS);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -866,9 +970,8 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     }
   };
 
-  // Ring of DEPTH batch buffers: DEPTH - 1 batches stay in flight while
-  // one is contracted.  Indices are compile-time, so the ring lives in
-  // registers.
+  // Ring of DEPTH batch buffers; indices are compile-time, so the ring lives
+  // in registers.
   for (uint32_t t = 0; t < NB; t += DEPTH) {
 #pragma unroll
     for (int r = 0; r < DEPTH; ++r) {
@@ -882,10 +985,10 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
 }
 
 // Multi-stripe FP8 kernel: the AQ4 multi-stripe kernel's structure (x staged
-// once per workgroup, a run of a.spw stripes, one ping-pong software pipeline
-// per wave over the run) with 64-k FP8 units.  Each batch also carries the
-// row scales of its stripe, applied once in the per-stripe reduction.
-// Requires units % (WAVES * B) == 0.
+// once per workgroup in the padded layout, a run of a.spw stripes, one ring
+// pipeline per wave over the run) with 64-k FP8 units.  Each batch also
+// carries the row scales of its stripe, applied once in the per-stripe
+// reduction.  Requires units % (WAVES * B) == 0.
 template <int MT, int WAVES, int B, int DEPTH>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     GemvArgs a) {
@@ -906,8 +1009,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
       nS * units * 1024);
   const __amdgpu_buffer_rsrc_t sbuf = byte_buffer(
       static_cast<const float *>(a.aux) + uint64_t(T0) * 16, nS * 64);
+  const uint32_t wlane = lane * 16, slane = (lane % 16) * 4;
   const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
   const uint32_t cpr = a.k / 8;
+  const uint32_t pitch = cpr + 1;
 
   struct Batch {
     u32x4 w[B];
@@ -920,11 +1025,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     for (int i = 0; i < B; ++i) {
       bt.w[i] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     wbuf, (item + i) * 1024 + lane * 16, 0, kNt));
+                     wbuf, wlane, (item + i) * 1024, kNt));
     }
     bt.rs = __builtin_bit_cast(
-        float, __builtin_amdgcn_raw_buffer_load_b32(
-                   sbuf, (ls * 16 + lane % 16) * 4, 0, 0));
+        float, __builtin_amdgcn_raw_buffer_load_b32(sbuf, slane, ls * 64, 0));
     lu += B;
     if (lu == ue) {
       lu = ub;
@@ -932,7 +1036,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     }
   };
 
-  stage_x_lds<WAVES>(a, xs, rows, cpr);
+  stage_x_pad<WAVES>(a, xs, rows, cpr);
   __builtin_amdgcn_sched_barrier(0);
   Batch ring[DEPTH];
 #pragma unroll
@@ -940,20 +1044,17 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     issue(ring[r]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<(DEPTH - 1) * (B + 1)>();  // this thread's activation copies have landed
+  wait_vmcnt<(DEPTH - 1) * (B + 1)>();  // this thread's activation copies landed
   lds_barrier();
 
-  const uint32_t cgk = 2 * (lane / 16);
-  const char *xa[MT][2];
+  // A operand of unit u, half h: chunk 8 u + 2 (lane / 16) + h of the row.
+  const char *xa[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const uint32_t m = mt * 16 + lane % 16;
     const uint32_t r = m < rows ? m : rows;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      xa[mt][h] = reinterpret_cast<const char *>(xs) +
-                  (r * cpr + ((cgk + h) ^ (r & 7u))) * 16;
-    }
+    xa[mt] = reinterpret_cast<const char *>(xs) +
+             (r * pitch + 2 * (lane / 16)) * 16;
   }
   f32x4 acc4[4][MT];
   auto zero_acc = [&]() {
@@ -984,9 +1085,9 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         acc4[ca][mt] = mfma_bf16(
-            *reinterpret_cast<const bf16x8 *>(xa[mt][0] + off), w0, acc4[ca][mt]);
+            *reinterpret_cast<const bf16x8 *>(xa[mt] + off), w0, acc4[ca][mt]);
         acc4[ca + 1][mt] = mfma_bf16(
-            *reinterpret_cast<const bf16x8 *>(xa[mt][1] + off), w1,
+            *reinterpret_cast<const bf16x8 *>(xa[mt] + off + 16), w1,
             acc4[ca + 1][mt]);
       }
     }
@@ -1004,9 +1105,6 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     }
   };
 
-  // Ring of DEPTH batch buffers: DEPTH - 1 batches stay in flight while
-  // one is contracted.  Indices are compile-time, so the ring lives in
-  // registers.
   for (uint32_t t = 0; t < NB; t += DEPTH) {
 #pragma unroll
     for (int r = 0; r < DEPTH; ++r) {
@@ -1166,13 +1264,13 @@ uint32_t resident_blocks(Kernel kernel, uint32_t threads, uint32_t lds) {
 // Multi-stripe kernel configurations (waves, units per batch, ring depth),
 // chosen by measurement on MI355X; overridable at build time for tuning.
 #ifndef ULLM_AQ4_MS_CFG
-#define ULLM_AQ4_MS_CFG 8, 2, 2
+#define ULLM_AQ4_MS_CFG 8, 2, 2, 8
 #endif
 #ifndef ULLM_FP8_MS_CFG
-#define ULLM_FP8_MS_CFG 8, 4, 2
+#define ULLM_FP8_MS_CFG 8, 4, 2, 8
 #endif
 struct MsCfg {
-  int waves, batch, depth;
+  int waves, batch, depth, ks;  // ks: waves splitting one stripe's K
 };
 constexpr MsCfg kAq4Ms{ULLM_AQ4_MS_CFG};
 constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
@@ -1191,13 +1289,13 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   if (!vec || !lds_allowed() || forced == 0) {
     return false;
   }
-  const uint32_t lds = lds_bytes(a, aq4);
+  const uint32_t lds = ms_lds_bytes(a, aq4);
   const uint32_t stripes = a.n16 / 16;
   // Dynamic (activation block) plus static (two reduction buffers) LDS must
   // fit the CU's 160 KiB; a run's weights must stay below 2 GiB (32-bit
   // buffer offsets; checked for the whole matrix, the longest possible run).
   if (lds > kXLdsBytes || lds + 2u * c.waves * mt * 1024u > 160u * 1024u ||
-      a.units % uint32_t(c.waves * c.batch) != 0 ||
+      a.units % uint32_t(c.ks * c.batch) != 0 ||
       uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31)) {
     return false;
   }
@@ -1219,27 +1317,30 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
 
 template <typename Kernel>
 hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
-                     hipStream_t s) {
+                     hipStream_t s, uint32_t subgroups = 1) {
   const uint32_t stripes = a.n16 / 16;
   const uint32_t target = resident_blocks(kernel, waves * kWave, lds);
   static const int forced = env_int("ULLM_GEMV_SPW", 0);
-  a.spw = forced > 0 ? uint32_t(forced) : (stripes + target - 1) / target;
+  // Runs are whole multiples of the sub-group count, so no sub-group idles.
+  const uint32_t spw = forced > 0 ? uint32_t(forced) : (stripes + target - 1) / target;
+  a.spw = (spw + subgroups - 1) / subgroups * subgroups;
   const dim3 grid((stripes + a.spw - 1) / a.spw, (a.m + 31) / 32);
   return launch_lds(kernel, grid, dim3(waves * kWave), lds, s, a);
 }
 
-template <int MT>
+template <int MT, int NR>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
-      aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.batch, kAq4Ms.depth>, a,
-      kAq4Ms.waves, lds_bytes(a, true), s);
+      aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch,
+                         kAq4Ms.depth, NR>,
+      a, kAq4Ms.waves, ms_lds_bytes(a, true), s, kAq4Ms.waves / kAq4Ms.ks);
 }
 
 template <int MT>
 hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
       fp8_gemv_ms_kernel<MT, kFp8Ms.waves, kFp8Ms.batch, kFp8Ms.depth>, a,
-      kFp8Ms.waves, lds_bytes(a, false), s);
+      kFp8Ms.waves, ms_lds_bytes(a, false), s);
 }
 
 template <int MT, int WAVES>
@@ -1297,7 +1398,12 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
   if (use_ms(a, vec, two ? 2 : 1, true)) {
-    return two ? launch_aq4_ms<2>(a, s) : launch_aq4_ms<1>(a, s);
+    if (two) {
+      return launch_aq4_ms<2, 4>(a, s);
+    }
+    return a.m == 1 ? launch_aq4_ms<1, 1>(a, s)
+                    : a.m == 2 ? launch_aq4_ms<1, 2>(a, s)
+                               : launch_aq4_ms<1, 4>(a, s);
   }
   const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
