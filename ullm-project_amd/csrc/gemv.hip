@@ -1117,6 +1117,378 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
   }
 }
 
+// Register-staged multi-stripe FP8 kernel, for activation blocks too large
+// for LDS (M > 16 at K = 4096, or long K).  Each wave reads its K share of
+// the activations straight from L2 into registers and reuses them across S
+// adjacent stripes ("stripe group"), so x is read from L2 once per S stripes
+// instead of once per stripe; a workgroup walks a run of a.spw stripe groups
+// with its WAVES waves splitting K, one ring pipeline per wave (weights, x
+// and the row scales of a batch travel together), and the partial sums of a
+// stripe group meet in LDS.  Rows past M are read at an offset outside the
+// activation buffer (zeros, no memory access).  Requires units % (WAVES * B)
+// == 0.
+template <int MT, int WAVES, int S, int B, int DEPTH>
+__global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
+    GemvArgs a) {
+  __shared__ float red[2][WAVES * S * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t units = a.units;
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t G = (stripes + S - 1) / S;  // stripe groups
+  const uint32_t G0 = blockIdx.x * a.spw;
+  const uint32_t nG = min(a.spw, G - G0);
+  const uint32_t T0 = G0 * S;
+  const uint32_t nT = min(nG * S, stripes - T0);  // stripes of the run
+  const uint32_t ub = units * wave / WAVES;
+  const uint32_t ue = units * (wave + 1) / WAVES;
+  const uint32_t nbw = (ue - ub) / B;
+  const uint32_t NB = nG * nbw;
+  const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
+      static_cast<const uint8_t *>(a.tiles) + uint64_t(T0) * units * 1024,
+      nT * units * 1024);
+  const __amdgpu_buffer_rsrc_t sbuf = byte_buffer(
+      static_cast<const float *>(a.aux) + uint64_t(T0) * 16, nT * 64);
+  const uint32_t m0 = blockIdx.y * 32;
+  const uint32_t rows = min(32u, a.m - m0);
+  const __amdgpu_buffer_rsrc_t xbuf = byte_buffer(
+      a.x + uint64_t(m0) * a.ldx, uint32_t(((rows - 1) * a.ldx + a.k) * 2));
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 16 * (lane / 16)) * 2)
+                        : 0x80000000u;
+  }
+  const uint32_t wlane = lane * 16, slane = (lane % 16) * 4;
+
+  struct Batch {
+    u32x4 w[B][S];
+    bf16x8 x[B][MT][2];
+    float rs[S];
+  };
+  // Load pointer: stripe group lg of the run, unit lu (scalars).  Past the
+  // run the weight and scale loads fall outside their buffers and the
+  // activation loads are pushed outside theirs, so they read zeros.
+  uint32_t lg = 0, lu = ub;
+  auto issue = [&](Batch &bt) {
+    const uint32_t xpast = lg < nG ? 0u : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          bt.x[i][mt][h] = __builtin_bit_cast(
+              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                          xbuf, xoff[mt], ((lu + i) * 128 + h * 16) | xpast, 0));
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        bt.w[i][s] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       wbuf, wlane, ((lg * S + s) * units + lu + i) * 1024, kNt));
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      bt.rs[s] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(sbuf, slane,
+                                                      (lg * S + s) * 64, 0));
+    }
+    lu += B;
+    if (lu == ue) {
+      lu = ub;
+      ++lg;
+    }
+  };
+
+  Batch ring[DEPTH];
+#pragma unroll
+  for (int r = 0; r + 1 < DEPTH; ++r) {
+    issue(ring[r]);
+  }
+  f32x4 acc[S][MT];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[s][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  zero_acc();
+  uint32_t cgp = 0, cu = ub;
+  auto consume = [&](const Batch &bt) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const u32x4 wv = bt.w[i][s];
+        const u32x2 b01 = e4m3x4_to_bf16x4(wv.x);
+        const u32x2 b23 = e4m3x4_to_bf16x4(wv.y);
+        const u32x2 b45 = e4m3x4_to_bf16x4(wv.z);
+        const u32x2 b67 = e4m3x4_to_bf16x4(wv.w);
+        const bf16x8 w0 =
+            __builtin_bit_cast(bf16x8, u32x4{b01.x, b01.y, b23.x, b23.y});
+        const bf16x8 w1 =
+            __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[s][mt] = mfma_bf16(bt.x[i][mt][0], w0, acc[s][mt]);
+          acc[s][mt] = mfma_bf16(bt.x[i][mt][1], w1, acc[s][mt]);
+        }
+      }
+    }
+    cu += B;
+    if (cu == ue) {  // stripe group done: reduce across waves, store, reset
+      float *rb = red[cgp & 1];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            rb[(((wave * S + s) * MT + mt) * 4 + r) * kWave + lane] = acc[s][mt][r];
+          }
+        }
+      }
+      lds_barrier();
+      const uint32_t Tg = T0 + cgp * S;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        for (uint32_t o = threadIdx.x; o < MT * 256; o += WAVES * kWave) {
+          const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
+          const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+          float v = 0.0f;
+#pragma unroll
+          for (int w = 0; w < WAVES; ++w) {
+            v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+          }
+          const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
+          if (m < a.m && n < a.n) {
+            v = a.alpha * (bt.rs[s] * v);
+            if (a.y_f32) {
+              static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
+            } else {
+              static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
+                  f32_to_bf16(v);
+            }
+          }
+        }
+      }
+      zero_acc();
+      cu = ub;
+      ++cgp;
+    }
+  };
+
+  for (uint32_t t = 0; t < NB; t += DEPTH) {
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+      issue(ring[(r + DEPTH - 1) % DEPTH]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + r < NB) {
+        consume(ring[r]);
+      }
+    }
+  }
+}
+
+// Register-staged multi-stripe AQ4 kernel: the FP8 register-staged kernel's
+// structure with 128-k groups.  Each wave reads its K share of x from L2
+// into registers once per group of S adjacent stripes; the per-group
+// activation sums come from one MFMA against a ones operand, shared by the S
+// stripes, so a group costs 4 (S + 1) MFMAs per m-tile plus the fp32
+// correction of each stripe.  Requires groups % (WAVES * B) == 0.
+template <int MT, int WAVES, int S, int B, int DEPTH>
+__global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
+    GemvArgs a) {
+  __shared__ float red[2][WAVES * S * MT * 4 * kWave];
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t groups = a.units;
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t G = (stripes + S - 1) / S;  // stripe groups
+  const uint32_t G0 = blockIdx.x * a.spw;
+  const uint32_t nG = min(a.spw, G - G0);
+  const uint32_t T0 = G0 * S;
+  const uint32_t nT = min(nG * S, stripes - T0);
+  const uint32_t ub = groups * wave / WAVES;
+  const uint32_t ue = groups * (wave + 1) / WAVES;
+  const uint32_t nbw = (ue - ub) / B;
+  const uint32_t NB = nG * nbw;
+  const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
+      static_cast<const uint8_t *>(a.tiles) + uint64_t(T0) * groups * 1024,
+      nT * groups * 1024);
+  const __amdgpu_buffer_rsrc_t zbuf = byte_buffer(
+      static_cast<const uint32_t *>(a.aux) + uint64_t(T0) * groups * 16,
+      nT * groups * 64);
+  const uint32_t m0 = blockIdx.y * 32;
+  const uint32_t rows = min(32u, a.m - m0);
+  const __amdgpu_buffer_rsrc_t xbuf = byte_buffer(
+      a.x + uint64_t(m0) * a.ldx, uint32_t(((rows - 1) * a.ldx + a.k) * 2));
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t m = mt * 16 + lane % 16;
+    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 8 * (lane / 16)) * 2)
+                        : 0x80000000u;
+  }
+  const uint32_t wlane = lane * 16, zlane = (lane % 16) * 4;
+  const bf16x8 ones = __builtin_bit_cast(
+      bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+  const uint32_t nmask = opaque_u32(0x000f000fu);
+  const uint32_t nmagic = opaque_u32(0x43004300u);
+
+  struct Batch {
+    u32x4 w[B][S];
+    uint32_t sz[B][S];
+    bf16x8 x[B][MT][4];
+  };
+  uint32_t lg = 0, lu = ub;
+  auto issue = [&](Batch &bt) {
+    const uint32_t xpast = lg < nG ? 0u : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bt.x[i][mt][j] = __builtin_bit_cast(
+              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                          xbuf, xoff[mt], ((lu + i) * 256 + j * 64) | xpast, 0));
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const uint32_t item = (lg * S + s) * groups + lu + i;
+        bt.w[i][s] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(wbuf, wlane,
+                                                         item * 1024, kNt));
+        bt.sz[i][s] =
+            __builtin_amdgcn_raw_buffer_load_b32(zbuf, zlane, item * 64, 0);
+      }
+    }
+    lu += B;
+    if (lu == ue) {
+      lu = ub;
+      ++lg;
+    }
+  };
+
+  Batch ring[DEPTH];
+#pragma unroll
+  for (int r = 0; r + 1 < DEPTH; ++r) {
+    issue(ring[r]);
+  }
+  f32x4 acc[S][MT];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[s][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  zero_acc();
+  uint32_t cgp = 0, cu = ub;
+  auto consume = [&](const Batch &bt) {
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      f32x4 xsum[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xsum[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xsum[mt] = mfma_bf16(bt.x[i][mt][j], ones, xsum[mt]);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        f32x4 p[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          p[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][s][j], nmask, nmagic);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            p[mt] = mfma_bf16(bt.x[i][mt][j], bj, p[mt]);
+          }
+        }
+        const float sf = f16_to_f32(uint16_t(bt.sz[i][s] & 0xffffu));
+        const float zoff = 128.0f + f16_to_f32(uint16_t(bt.sz[i][s] >> 16));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            acc[s][mt][r] += sf * (p[mt][r] - zoff * xsum[mt][r]);
+          }
+        }
+      }
+    }
+    cu += B;
+    if (cu == ue) {  // stripe group done: reduce across waves, store, reset
+      float *rb = red[cgp & 1];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            rb[(((wave * S + s) * MT + mt) * 4 + r) * kWave + lane] = acc[s][mt][r];
+          }
+        }
+      }
+      lds_barrier();
+      const uint32_t Tg = T0 + cgp * S;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        for (uint32_t o = threadIdx.x; o < MT * 256; o += WAVES * kWave) {
+          const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
+          const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+          float v = 0.0f;
+#pragma unroll
+          for (int w = 0; w < WAVES; ++w) {
+            v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+          }
+          const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
+          if (m < a.m && n < a.n) {
+            v = a.alpha * v;
+            if (a.y_f32) {
+              static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
+            } else {
+              static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
+                  f32_to_bf16(v);
+            }
+          }
+        }
+      }
+      zero_acc();
+      cu = ub;
+      ++cgp;
+    }
+  };
+
+  for (uint32_t t = 0; t < NB; t += DEPTH) {
+#pragma unroll
+    for (int r = 0; r < DEPTH; ++r) {
+      issue(ring[(r + DEPTH - 1) % DEPTH]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + r < NB) {
+        consume(ring[r]);
+      }
+    }
+  }
+}
+
 // Waves per workgroup (they split K).  Measured on MI355X: FP8 streams best
 // with 8 waves per stripe at every Llama shape; AQ4 (half the bytes per
 // stripe) with 4 once the grid has enough stripes to fill the chip.
@@ -1275,6 +1647,26 @@ struct MsCfg {
 constexpr MsCfg kAq4Ms{ULLM_AQ4_MS_CFG};
 constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 
+// Register-staged kernel configurations by grid size (measured on MI355X,
+// K = 4096 unless noted, against the kernel the launch used before):
+//   wide   (>= 4096 stripes): 8 waves, groups of 4 stripes;
+//          AQ4 M=8 4096->128256 54.5 against 59.7 us;
+//   large  (>= 1024 stripes): 4 waves, groups of 4; AQ4 M=32 4096->28672
+//          25.6 against 56.7 us, M=8 15.6 against 18.2 us; FP8 M=32 29.1
+//          against 58.3 us;
+//   medium (>= 384 stripes): 4 waves, groups of 2; AQ4 M=32 4096->6144 11.2
+//          against 17.9 us, M=8 6.4 against 7.9 us;
+//   deep K (< 384 stripes, K >= 8192): 16 waves, single stripes; AQ4 M=8
+//          14336->4096 13.0 against 14.3 us.
+// Each is {waves, units per batch, ring depth, stripes per group}.
+struct RsCfg {
+  int waves, batch, depth, s;
+};
+constexpr RsCfg kRsWide{8, 1, 2, 4};
+constexpr RsCfg kRsLarge{4, 1, 2, 4};
+constexpr RsCfg kRsMedium{4, 1, 2, 2};
+constexpr RsCfg kRsDeepK{16, 1, 2, 1};
+
 // Whether the multi-stripe kernel takes this launch.  It stages the
 // activation block once per workgroup and amortises it over a run of
 // stripes.  Measured on MI355X (AQ4, K = 4096, 8 waves, batches of 2
@@ -1343,6 +1735,64 @@ hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
       kFp8Ms.waves, ms_lds_bytes(a, false), s);
 }
 
+// Configuration of the register-staged kernel for this launch, or nullptr:
+// it needs aligned activations, whole batches per wave, 32-bit buffer
+// offsets for the weights and the activation block, and pays from M = 4 on
+// (below, the LDS-staged kernels stay ahead).  ULLM_GEMV_RS=0 disables it,
+// ULLM_GEMV_RS=1 forces it at any M.
+const RsCfg *plan_rs(const GemvArgs &a, bool vec) {
+  static const int forced = env_int("ULLM_GEMV_RS", -1);
+  const uint32_t rows = min(a.m, 32u);
+  const uint32_t stripes = a.n16 / 16;
+  if (forced == 0 || !vec || (a.m < 4 && forced != 1) ||
+      uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31) ||
+      (uint64_t(rows - 1) * a.ldx + a.k) * 2 >= (uint64_t(1) << 31)) {
+    return nullptr;
+  }
+  const RsCfg *c = stripes >= 4096   ? &kRsWide
+                   : stripes >= 1024 ? &kRsLarge
+                   : stripes >= 384  ? &kRsMedium
+                   : a.k >= 8192     ? &kRsDeepK
+                                     : nullptr;
+  if (c == nullptr && forced == 1) {
+    c = &kRsMedium;
+  }
+  if (c == nullptr || a.units % uint32_t(c->waves * c->batch) != 0) {
+    return nullptr;
+  }
+  return c;
+}
+
+template <typename Kernel>
+hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
+                     hipStream_t s) {
+  const uint32_t groups = (a.n16 / 16 + C.s - 1) / C.s;
+  const uint32_t target = resident_blocks(kernel, C.waves * kWave, 0);
+  static const int forced = env_int("ULLM_GEMV_SPW", 0);
+  a.spw = forced > 0 ? uint32_t(forced) : (groups + target - 1) / target;
+  const dim3 grid((groups + a.spw - 1) / a.spw, (a.m + 31) / 32);
+  hipLaunchKernelGGL(kernel, grid, dim3(C.waves * kWave), 0, s, a);
+  return hipGetLastError();
+}
+
+#define ULLM_RS_KERNEL(K, MT, C) K<MT, C.waves, C.s, C.batch, C.depth>
+template <int MT>
+hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
+  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide), *c, a, s);
+  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge), *c, a, s);
+  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK), *c, a, s);
+}
+
+template <int MT>
+hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
+  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide), *c, a, s);
+  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge), *c, a, s);
+  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK), *c, a, s);
+}
+#undef ULLM_RS_KERNEL
+
 template <int MT, int WAVES>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
@@ -1378,8 +1828,15 @@ bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 64);
   const bool two = a.m > 16;
+  // FP8 keeps the LDS-staged kernel where the activation block fits (M=8
+  // 4096->28672: 21.0 against 25.3 us register-staged); AQ4, whose per-byte
+  // work is heavier, gains from the register-staged kernel there too.
   if (use_ms(a, vec, two ? 2 : 1, false)) {
     return two ? launch_fp8_ms<2>(a, s) : launch_fp8_ms<1>(a, s);
+  }
+  // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
+  if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec) : nullptr) {
+    return two ? launch_fp8_rs<2>(a, rs, s) : launch_fp8_rs<1>(a, rs, s);
   }
   const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
@@ -1397,6 +1854,9 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
+  if (const RsCfg *rs = plan_rs(a, vec)) {
+    return two ? launch_aq4_rs<2>(a, rs, s) : launch_aq4_rs<1>(a, rs, s);
+  }
   if (use_ms(a, vec, two ? 2 : 1, true)) {
     if (two) {
       return launch_aq4_ms<2, 4>(a, s);
