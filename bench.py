@@ -290,7 +290,7 @@ def main():
                      "frac": round(head["GB_s"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("aq4_gemv_m1_k4096_n14336"),
                      "kernel_us": round(us, 3),
-                     "kernel": "aq4_gemv_lds_kernel"},
+                     "kernel": "aq4_gemv_ms_kernel"},
         "cpu_baseline": cpu,
         "configs": configs,
     }
