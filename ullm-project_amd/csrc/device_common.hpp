@@ -154,4 +154,16 @@ __device__ __forceinline__ float wave_min(float v) {
   return v;
 }
 
+// Byte-range buffer over device memory: loads at offsets past `bytes` return
+// zero without a memory access, which lets a software pipeline issue its
+// look-ahead loads unconditionally (a branch around a load makes the compiler
+// drain every outstanding load at the join).  Offsets are 32-bit: the range
+// must stay below 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *p,
+                                                             uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
+                                           static_cast<int>(bytes), 0x00020000);
+}
+constexpr int kNt = 2;                      // nontemporal cache policy bit
+
 }  // namespace ullm

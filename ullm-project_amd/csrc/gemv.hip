@@ -684,17 +684,6 @@ __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
   }
 }
 
-// Byte-range buffer over device memory for the multi-stripe kernels: loads at
-// offsets past `bytes` return zero without a memory access, which lets the
-// software pipeline issue its look-ahead loads unconditionally (a branch
-// around a load makes the compiler drain every outstanding load at the join).
-// Offsets are 32-bit: a run must stay below 2 GiB.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *p,
-                                                             uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0,
-                                           static_cast<int>(bytes), 0x00020000);
-}
-constexpr int kNt = 2;                      // nontemporal cache policy bit
 
 // Activation block layout of the multi-stripe kernels: row r's 16-byte
 // chunk c at slot r * (cpr + 1) + c.  The one-chunk row padding puts the 16
