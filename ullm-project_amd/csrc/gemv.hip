@@ -1651,10 +1651,22 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 struct RsCfg {
   int waves, batch, depth, s;
 };
-constexpr RsCfg kRsWide{8, 1, 2, 4};
-constexpr RsCfg kRsLarge{4, 1, 2, 4};
-constexpr RsCfg kRsMedium{4, 1, 2, 2};
-constexpr RsCfg kRsDeepK{16, 1, 2, 1};
+#ifndef ULLM_RS_WIDE
+#define ULLM_RS_WIDE 8, 1, 2, 4
+#endif
+#ifndef ULLM_RS_LARGE
+#define ULLM_RS_LARGE 4, 1, 2, 4
+#endif
+#ifndef ULLM_RS_MEDIUM
+#define ULLM_RS_MEDIUM 4, 1, 2, 2
+#endif
+#ifndef ULLM_RS_DEEPK
+#define ULLM_RS_DEEPK 16, 1, 2, 1
+#endif
+constexpr RsCfg kRsWide{ULLM_RS_WIDE};
+constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
+constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
+constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 
 // Whether the multi-stripe kernel takes this launch.  It stages the
 // activation block once per workgroup and amortises it over a run of
