@@ -131,6 +131,38 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
                  what=f"{enc} gemv bf16 many stripes")
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (17, 6200, 4096),    # two m-tiles, 388 stripes: register-staged, groups of 2
+    (32, 16400, 1024),   # 1025 stripes: groups of 4
+    (8, 65600, 1024),    # 4100 stripes: the wide configuration
+    (8, 1000, 8192),     # 63 stripes, long K: single-stripe groups, 16 waves
+    (33, 6200, 1024),    # a second 32-row block of one row
+])
+@pytest.mark.parametrize("enc", ["fp8", "aq4"])
+def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
+    """Shapes that select each grid-size tier of the register-staged
+    multi-stripe kernels (M >= 8 for FP8, M >= 4 for AQ4; FP8 only where its
+    activation block does not fit LDS), including the two-m-tile variant and
+    a ragged last stripe and stripe group."""
+    w = weights(n, k, tag=31)
+    xb = activations_bf16(orc, m, k, tag=m + 300)
+    if enc == "fp8":
+        q, s = orc.fp8_quantize_rows(w)
+        y_ref, _ = orc.fp8_gemv(xb, q, s)
+        lw = uh.LinearWeight.from_fp8(q, s)
+    else:
+        p, s, z = orc.aq4_quantize(w)
+        y_ref, _ = orc.aq4_gemv(xb, p, s, z)
+        lw = uh.LinearWeight.from_aq4(p, s, z)
+    x = to_torch_bf16(xb, gpu)
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} gemv f32 {m}x{n}x{k}")
+    yb = lw.forward(x)
+    assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True,
+                 what=f"{enc} gemv bf16 {m}x{n}x{k}")
+
+
 def test_gemv_strided_activation_and_alpha(uh, orc, gpu):
     n, k, m = 48, 384, 5
     w = weights(n, k, tag=9)
