@@ -118,18 +118,22 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
 // LDS-pipelined kernel (v_mfma_f32_16x16x128_f8f6f4, fp8 x fp8).
 //
 // Block tile BM x BN x 128 (k), WM x WN waves, each wave owning a
-// (BM / WM) x (BN / WN) output tile of 16 x 16 MFMA tiles.  Both operands are
-// staged as 1 KiB "wave tiles": 16 rows x 64 k in MFMA lane order (lane l =
-// row l % 16, 16 bytes at k = 16 * (l / 16)), the order the weights already
-// have in HBM.  A lane's 32-byte MFMA operand is its 16 bytes of the k-block
-// [0, 64) tile followed by those of [64, 128), for A and B alike, so the k
-// pairing matches and every LDS read is a lane-contiguous ds_read_b128 (no
-// bank conflicts).  Global -> LDS moves are direct global_load_lds_dwordx4
+// (BM / WM) x (BN / WN) output tile of 16 x 16 MFMA tiles.  B is staged as
+// 1 KiB "wave tiles": 16 rows x 64 k in MFMA lane order (lane l = row l % 16,
+// 16 bytes at k = 16 * (l / 16)), the order the weights already have in HBM.
+// A (row-major activations) is staged as whole 128-byte row segments with
+// swizzled chunks (layout at the copy offsets below).  A lane's 32-byte MFMA
+// operand is its 16 bytes of k [0, 64) followed by those of [64, 128), for A
+// and B alike, so the k pairing matches; every LDS read is a ds_read_b128
+// without bank conflicts.  Global -> LDS moves are direct global_load_lds_dwordx4
 // (no registers); two stages alternate so the copies of step s + 1 run under
 // the MFMAs of step s.  The default 256 x 256 block (8 waves of 128 x 64)
-// measured fastest on MI355X: 1.77 PFLOP/s at M=2048, N=28672, K=4096 with
-// random operands, against 1.37 for a 128 x 128 block that fits two
-// workgroups per CU but doubles the operand traffic from L2.
+// measured fastest on MI355X, 1.96 PFLOP/s at M=2048, N=28672, K=4096 with
+// random operands (1.37 for a 128 x 128 block that fits two workgroups per
+// CU but doubles the operand traffic from L2).  Activation rows are copied
+// as whole 128-byte lines (see the A stage layout below): copying them as
+// 16-row wave tiles, 64 bytes per row per copy, capped the copy pipeline at
+// 8 TB/s from L2 and the kernel at 1.75 PFLOP/s.
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
@@ -225,11 +229,17 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   // of the stage.  Rows past M and stripes past N repeat the last valid one;
   // their results are never stored.
   uint32_t aoff[C::A_COPIES], boff[C::B_COPIES];
+  // A stage: 128 k-bytes of each of the block's rows, row-major (row r at
+  // r * 128), its eight 16-byte chunks XOR-swizzled with (r >> 1) & 7.  Each
+  // copy moves 8 whole rows: lane L fills slot L % 8 of row L / 8 from the
+  // row's chunk (L % 8) ^ swizzle, so every 8 lanes read one full 128-byte
+  // line of x, and the 16 rows an MFMA operand read touches (at one chunk)
+  // land in 16 different bank groups.
 #pragma unroll
   for (uint32_t i = 0; i < C::A_COPIES; ++i) {
-    const uint32_t t = (i * C::WAVES + wave) / 2, kb = (i * C::WAVES + wave) % 2;
-    const uint32_t m = min(m0 + t * 16 + lane % 16, a.m - 1);
-    aoff[i] = m * uint32_t(a.ldxq) + kb * 64 + (lane / 16) * 16;
+    const uint32_t r = (i * C::WAVES + wave) * 8 + lane / 8;
+    const uint32_t m = min(m0 + r, a.m - 1);
+    aoff[i] = m * uint32_t(a.ldxq) + (((lane % 8) ^ ((r >> 1) & 7)) * 16);
   }
 #pragma unroll
   for (uint32_t i = 0; i < C::B_COPIES; ++i) {
@@ -259,6 +269,16 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     }
   };
   constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
+  const uint32_t swz = (lane % 16) >> 1 & 7;
+  const uint32_t a_lo = ((lane / 16) ^ swz) * 16;
+  const uint32_t a_hi = ((4 + lane / 16) ^ swz) * 16;
+  auto a_operand = [&](const char *rows, uint32_t i) {
+    const char *p = rows + i * 16 * 128;
+    const u32x4 lo = *reinterpret_cast<const u32x4 *>(p + a_lo);
+    const u32x4 hi = *reinterpret_cast<const u32x4 *>(p + a_hi);
+    const u32x8 v = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    return __builtin_bit_cast(i32x8, v);
+  };
 
   f32x4 acc[C::TM][C::TN];
 #pragma unroll
@@ -290,7 +310,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     if (b_more) {
       copy_b(ks + BAHEAD);
     }
-    const char *As = a_buf(ks) + (wm * C::TM * 2) * 1024 + lane * 16;
+    // Lane l's operand of m-tile i: row 16 i + l % 16 of the wave's rows,
+    // k-bytes 16 (l / 16) .. (lo) and 64 + 16 (l / 16) .. (hi).
+    const char *As = a_buf(ks) + (wm * C::TM * 16 + lane % 16) * 128;
     const char *Bs = b_buf(ks) + (wn * C::TN * 2) * 1024 + lane * 16;
     i32x8 bf[C::TN];
 #pragma unroll
@@ -298,12 +320,12 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       bf[j] = lds_operand(Bs + j * 2048);
     }
     // The A operand of m-tile i + 1 is read while the MFMAs of m-tile i run.
-    i32x8 af = lds_operand(As);
+    i32x8 af = a_operand(As, 0);
 #pragma unroll
     for (uint32_t i = 0; i < C::TM; ++i) {
       i32x8 an = af;
       if (i + 1 < C::TM) {
-        an = lds_operand(As + (i + 1) * 2048);
+        an = a_operand(As, i + 1);
       }
 #pragma unroll
       for (uint32_t j = 0; j < C::TN; ++j) {
