@@ -197,7 +197,10 @@ def test_activation_quant_bit_exact(uh, orc, gpu, m, k):
 @pytest.mark.parametrize("m,n,k", [(1, 16, 64), (7, 17, 65), (64, 64, 512),
                                    (130, 100, 1000), (256, 256, 4096),
                                    (200, 300, 512), (128, 17, 128),
-                                   (513, 1040, 1024)])
+                                   (513, 1040, 1024),
+                                   # 256 x 256 blocks fill one round exactly,
+                                   # so the 256-column block is chosen
+                                   (256, 65536, 256)])
 def test_fp8_gemm_parity(uh, orc, gpu, m, n, k):
     w = weights(n, k, tag=13)
     q, s = orc.fp8_quantize_rows(w)

@@ -156,8 +156,11 @@ struct GemmCfg {
   static constexpr uint32_t B_BYTES = B_TILES * 1024;
   static constexpr uint32_t STAGE_BYTES = 2 * A_BYTES + BSTAGES * B_BYTES;
   static constexpr uint32_t A_COPIES = A_TILES / WAVES;
-  static constexpr uint32_t B_COPIES = B_TILES / WAVES;
-  static_assert(A_TILES % WAVES == 0 && B_TILES % WAVES == 0, "copy split");
+  // B copies per wave; when the waves do not split B evenly, the last round
+  // of copies is done by the first B_TILES % WAVES waves only.
+  static constexpr uint32_t B_COPIES = (B_TILES + WAVES - 1) / WAVES;
+  static constexpr bool B_EVEN = B_TILES % WAVES == 0;
+  static_assert(A_TILES % WAVES == 0, "copy split");
   // Epilogue staging of each wave's bf16 tile; rows padded by 16 bytes so
   // the row groups of one LDS store land in different banks.
   static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
@@ -165,7 +168,6 @@ struct GemmCfg {
   static constexpr uint32_t LDS =
       OUT_BYTES > STAGE_BYTES ? OUT_BYTES : STAGE_BYTES;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
-  static_assert(kWave % (TN * 2) == 0, "epilogue row split");
 };
 
 __device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
@@ -243,7 +245,8 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   }
 #pragma unroll
   for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-    const uint32_t t = (i * C::WAVES + wave) / 2, kb = (i * C::WAVES + wave) % 2;
+    const uint32_t c = min(i * C::WAVES + wave, C::B_TILES - 1);
+    const uint32_t t = c / 2, kb = c % 2;
     const uint32_t T = min(T0 + t, stripes - 1);
     boff[i] = (T * a.units + kb) * 1024 + lane * 16;
   }
@@ -265,7 +268,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     char *st = b_buf(ks);
 #pragma unroll
     for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-      dma16(bbase + boff[i], st + (i * C::WAVES + wave) * 1024);
+      if (C::B_EVEN || i * C::WAVES + wave < C::B_TILES) {
+        dma16(bbase + boff[i], st + (i * C::WAVES + wave) * 1024);
+      }
     }
   };
   constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
@@ -333,7 +338,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       af = an;
     }
-    if (b_more && BAHEAD > 1) {
+    if (b_more && BAHEAD > 1 && C::B_EVEN) {
       wait_vm<C::B_COPIES>();
     } else {
       __builtin_amdgcn_s_waitcnt(0);
@@ -377,13 +382,17 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
-    constexpr uint32_t lpr = C::TN * 2, rpi = kWave / lpr;
-    const uint32_t c8 = (lane % lpr) * 8;
-    const uint32_t n = nw + c8;
+    // 16-byte segments: TN * 2 per row of the wave's tile, spread over the
+    // lanes row-major.
+    constexpr uint32_t lpr = C::TN * 2, segs = C::TM * 16 * lpr;
 #pragma unroll
-    for (uint32_t it = 0; it < C::TM * 16 / rpi; ++it) {
-      const uint32_t row = it * rpi + lane / lpr;
-      const uint32_t m = mw + row;
+    for (uint32_t it = 0; it < (segs + kWave - 1) / kWave; ++it) {
+      const uint32_t seg = it * kWave + lane;
+      if (segs % kWave != 0 && seg >= segs) {
+        break;
+      }
+      const uint32_t row = seg / lpr, c8 = (seg % lpr) * 8;
+      const uint32_t m = mw + row, n = nw + c8;
       const u32x4 v = *reinterpret_cast<const u32x4 *>(
           tile_out + row * C::OUT_STRIDE + c8);
       uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
@@ -424,7 +433,42 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
 }
 
 using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
+// 224 columns: 4 waves of 64 rows x 2 of 112 columns.  For N = 28672 (and
+// any N with whole 224-column blocks) the tile count becomes a multiple of
+// the CU count where 256-column tiles leave the last round half empty.
+using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_BSTAGES>;
 using GemmMid = GemmCfg<128, 128, 2, 2>;    // 2 workgroups per CU
+
+// Compute units of the current device.
+uint32_t gemm_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+          hipSuccess || n <= 0) {
+    return 256;
+  }
+  return uint32_t(n);
+}
+
+// One workgroup per CU at a time: the kernel takes ceil(tiles / CUs) rounds,
+// each as long as one tile, and a tile's time scales with its width.  Pick
+// the 224-column block when that makes the rounds shorter overall.
+// ULLM_GEMM_BN=256/224 forces a width.
+bool gemm_use_narrow(uint32_t m, uint32_t n) {
+  static const int forced = [] {
+    const char *e = std::getenv("ULLM_GEMM_BN");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced == 256 || forced == 224) {
+    return forced == 224;
+  }
+  static const uint32_t cus = gemm_cu_count();
+  const uint64_t mb = (m + 255) / 256;
+  const uint64_t t256 = mb * ((n + 255) / 256), t224 = mb * ((n + 223) / 224);
+  const uint64_t cost256 = (t256 + cus - 1) / cus * 256;
+  const uint64_t cost224 = (t224 + cus - 1) / cus * 224;
+  return cost224 < cost256;
+}
 
 template <class C>
 hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
@@ -476,7 +520,9 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            w->fp8.bytes() < (uint64_t(1) << 32);
   if (vec && offsets_fit && a.k % 128 == 0 && m >= 128) {
     return gemm_mid_forced() ? launch_gemm_lds<GemmMid>(a, s)
-                             : launch_gemm_lds<GemmLarge>(a, s);
+                             : gemm_use_narrow(m, a.n)
+                                   ? launch_gemm_lds<GemmNarrow>(a, s)
+                                   : launch_gemm_lds<GemmLarge>(a, s);
   }
   const dim3 grid((a.n + 63) / 64, (m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel, grid, dim3(256), 0, s, a, vec);
