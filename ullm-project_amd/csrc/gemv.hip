@@ -1700,7 +1700,9 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   // 7.9 us; at M = 1..4 the single-stripe kernel is level or ahead on the
   // larger shapes (M=1 4096->28672 20.2 against 21.5 us).
   if (!aq4) {
-    return a.m >= 8;
+    // ... and at M < 8 on grids of at most one stripe per CU (4096 -> 4096
+    // M=1: 4.79 against 5.03 us).
+    return a.m >= 8 || stripes <= cu_count();
   }
   // AQ4: runs of 3+ stripes at M >= 4, taking two resident workgroups per CU
   // when the activation block leaves room for two.
