@@ -182,7 +182,11 @@ def test_gemv_strided_activation_and_alpha(uh, orc, gpu):
     assert_close(y.cpu().numpy(), orc.fp8_gemv(xo, q, s)[0], what="unaligned")
 
 
-@pytest.mark.parametrize("m,k", [(1, 1), (3, 17), (7, 255), (16, 4096), (33, 513)])
+@pytest.mark.parametrize("m,k", [(1, 1), (3, 17), (7, 255), (16, 4096), (33, 513),
+                                 # 16-byte vector path: one, two, eight chunks
+                                 # per thread; nine falls back to scalar loads
+                                 (5, 8), (64, 2048), (3, 16384), (3, 16392),
+                                 (2048, 4096)])
 def test_activation_quant_bit_exact(uh, orc, gpu, m, k):
     xb = activations_bf16(orc, m, k, tag=k)
     if m > 2:
@@ -192,6 +196,20 @@ def test_activation_quant_bit_exact(uh, orc, gpu, m, k):
     xq, xs = uh.quantize_activations(to_torch_bf16(xb, gpu))
     assert np.array_equal(xq.cpu().numpy(), xq_ref)
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
+
+
+def test_activation_quant_strided_view(uh, orc, gpu):
+    """A 16-byte aligned view with a padded row stride takes the vector path;
+    an odd column offset the scalar one.  Both match the oracle."""
+    m, k = 9, 1024
+    wide = activations_bf16(orc, m, k + 24, tag=77)
+    big = to_torch_bf16(wide, gpu)
+    for off in (8, 3):
+        xb = np.ascontiguousarray(wide[:, off:off + k])
+        xq_ref, xs_ref = orc.act_quantize(xb)
+        xq, xs = uh.quantize_activations(big[:, off:off + k])
+        assert np.array_equal(xq.cpu().numpy(), xq_ref)
+        assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 16, 64), (7, 17, 65), (64, 64, 512),

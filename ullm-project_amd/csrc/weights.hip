@@ -239,6 +239,53 @@ __global__ __launch_bounds__(kBlock) void act_quant_kernel(
   }
 }
 
+// Vectorized activation quantization for 16-byte aligned rows with K a
+// multiple of 8: each thread keeps CH chunks of 8 bf16 of its row in
+// registers (one 16-byte load each), so the row is read once, and writes 8
+// codes per store.  The per-element arithmetic is that of act_quant_kernel.
+template <int CH>
+__global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
+    const uint16_t *__restrict__ x, uint64_t ldx, uint64_t k,
+    uint8_t *__restrict__ xq, float *__restrict__ xs) {
+  __shared__ float red[kBlock / kWave];
+  const uint64_t row = blockIdx.x;
+  const uint16_t *src = x + row * ldx;
+  u32x4 v[CH];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
+    v[c] = idx < k ? *reinterpret_cast<const u32x4 *>(src + idx)
+                   : u32x4{0u, 0u, 0u, 0u};
+    const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      amax = fmaxf(amax, fabsf(bf16_to_f32(uint16_t(w[e] & 0xffffu))));
+      amax = fmaxf(amax, fabsf(bf16_to_f32(uint16_t(w[e] >> 16))));
+    }
+  }
+  amax = block_max(amax, red);
+  const float a = amax / 448.0f;
+  if (threadIdx.x == 0) {
+    xs[row] = a;
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
+    if (idx < k) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+      uint32_t out[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t h = uint16_t(e % 2 ? w[e / 2] >> 16 : w[e / 2] & 0xffffu);
+        const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(h) / a);
+        out[e / 4] |= q << (8 * (e % 4));
+      }
+      *reinterpret_cast<u32x2 *>(xq + row * k + idx) = u32x2{out[0], out[1]};
+    }
+  }
+}
+
 unsigned grid_for(uint64_t total) {
   const uint64_t blocks = (total + kBlock - 1) / kBlock;
   return static_cast<unsigned>(blocks < 65536 ? (blocks ? blocks : 1) : 65536);
@@ -308,6 +355,17 @@ hipError_t launch_aq4_dequant(const uint32_t *tiles, const uint32_t *sz,
 
 hipError_t launch_act_quant(const uint16_t *x, uint64_t ldx, uint64_t m,
                             uint64_t k, uint8_t *xq, float *xs, hipStream_t s) {
+  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 8 == 0 &&
+                   k % 8 == 0 && reinterpret_cast<uintptr_t>(xq) % 8 == 0;
+  const uint64_t chunks = (k / 8 + kBlock - 1) / kBlock;  // per thread
+  if (vec && chunks <= 8) {
+    auto kernel = chunks <= 1   ? act_quant_vec_kernel<1>
+                  : chunks <= 2 ? act_quant_vec_kernel<2>
+                  : chunks <= 4 ? act_quant_vec_kernel<4>
+                                : act_quant_vec_kernel<8>;
+    hipLaunchKernelGGL(kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k, xq, xs);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(act_quant_kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k,
                      xq, xs);
   return hipGetLastError();
