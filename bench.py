@@ -142,10 +142,19 @@ def bench_gemm(r, m, n, k, steps, warmup):
     calls = [(lambda w=w: w.forward(xq, y, x_scales=xs)) for w in ws]
     ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
     tflops = 2.0 * m * n * k / (us_call * 1e-6) / 1e12
+    # End to end from bf16 activations: per-token quantization into the
+    # caller's workspace, then the GEMM (two kernels per call).
+    wsb = torch.empty((ws[0].workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN),),
+                      dtype=torch.uint8, device=r.dev)
+    calls = [(lambda w=w: w.forward(x, y, mode=uh.ACT_FP8_PER_TOKEN,
+                                    workspace=wsb)) for w in ws]
+    _, us_e2e, _ = r.time_sweep(calls, steps, warmup)
     for w in ws:
         w.destroy()
     return {"m": m, "n": n, "k": k, "us_per_launch": us_call,
             "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
+            "us_with_act_quant": us_e2e,
+            "TFLOPS_with_act_quant": 2.0 * m * n * k / (us_e2e * 1e-6) / 1e12,
             "timing": mode}
 
 

@@ -358,6 +358,21 @@ class LinearWeight:
         return out
 
     # -- compute -----------------------------------------------------------
+    def workspace_size(self, m, *, mode=ACT_EXACT, x_dtype=DTYPE_BF16):
+        """Bytes of caller workspace a forward of m rows needs
+        (ullm_linear_workspace_size); 0 when it needs none."""
+        import torch
+        probe = torch.empty((1,), dtype=torch.uint8)  # any non-null address
+        d = new(ForwardDesc, weight=self.handle, m=m, x=_ptr(probe),
+                x_row_stride=0, x_scales=_ptr(probe), y=_ptr(probe),
+                y_row_stride=0, x_dtype=x_dtype, y_dtype=DTYPE_BF16,
+                activation_mode=mode, alpha=1.0)
+        out = _u64(0)
+        s = _Sink()
+        _check(lib().ullm_linear_workspace_size(ctypes.byref(d), ctypes.byref(out),
+                                                s.ref), s)
+        return int(out.value)
+
     def forward(self, x, y=None, *, x_scales=None, out_dtype=None, alpha=1.0,
                 mode=ACT_EXACT, stream=None, workspace=None):
         """y = alpha * x @ W^T for x bf16 [M][>=K] (row stride honoured) or
