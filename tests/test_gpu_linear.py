@@ -137,6 +137,10 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     (8, 65600, 1024),    # 4100 stripes: the wide configuration
     (8, 1000, 8192),     # 63 stripes, long K: single-stripe groups, 16 waves
     (33, 6200, 1024),    # a second 32-row block of one row
+    (4, 1000, 8192),     # AQ4 single stripes, rows packed in four classes
+    (7, 1000, 8192),     # AQ4 single stripes, two classes, a ragged class
+    (5, 16400, 1024),    # AQ4 groups of 4 at M = 5
+    (6, 65600, 1024),    # AQ4 wide configuration at M = 6
 ])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
@@ -161,6 +165,33 @@ def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
     yb = lw.forward(x)
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True,
                  what=f"{enc} gemv bf16 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [4, 8])
+@pytest.mark.parametrize("enc", ["fp8", "aq4"])
+def test_gemv_register_staged_strided_rows(uh, orc, gpu, enc, m):
+    """Packed register-staged launches reading x as a column slice of a wider
+    buffer (the decode stack reads the q slice of the qkv output and the gate
+    half of the gate_up output this way)."""
+    # K = 16384: at M = 8 the FP8 activation block exceeds LDS, so FP8 too
+    # takes the register-staged kernel.
+    n, k = 1000, 16384
+    w = weights(n, k, tag=37)
+    wide = activations_bf16(orc, m, k + 264, tag=m + 310)
+    xb = np.ascontiguousarray(wide[:, :k])
+    if enc == "fp8":
+        q, s = orc.fp8_quantize_rows(w)
+        y_ref, _ = orc.fp8_gemv(xb, q, s)
+        lw = uh.LinearWeight.from_fp8(q, s)
+    else:
+        p, s, z = orc.aq4_quantize(w)
+        y_ref, _ = orc.aq4_gemv(xb, p, s, z)
+        lw = uh.LinearWeight.from_aq4(p, s, z)
+    x = to_torch_bf16(wide, gpu)[:, :k]
+    assert x.stride(0) == k + 264
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} gemv strided m={m}")
 
 
 def test_gemv_strided_activation_and_alpha(uh, orc, gpu):

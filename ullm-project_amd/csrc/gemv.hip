@@ -857,8 +857,10 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
 #pragma unroll
   for (int r = 0; r + 1 < DEPTH; ++r) {
     issue(ring[r]);
+    // Keep the batches in ring order: the steady-state waits assume that
+    // batch r's loads are all older than batch r + 1's.
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt<(DEPTH - 1) * 2 * B>();  // this thread's activation copies landed
   lds_barrier();
   // Group sums: 16 lanes per (row, group), one chunk each, then a butterfly.
@@ -1031,8 +1033,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 #pragma unroll
   for (int r = 0; r + 1 < DEPTH; ++r) {
     issue(ring[r]);
+    // Keep the batches in ring order: the steady-state waits assume that
+    // batch r's loads are all older than batch r + 1's.
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
   wait_vmcnt<(DEPTH - 1) * (B + 1)>();  // this thread's activation copies landed
   lds_barrier();
 
@@ -1115,10 +1119,15 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 // and the row scales of a batch travel together), and the partial sums of a
 // stripe group meet in LDS.  Rows past M are read at an offset outside the
 // activation buffer (zeros, no memory access).  Requires units % (WAVES * B)
-// == 0.
-template <int MT, int WAVES, int S, int B, int DEPTH>
+// == 0.  P = 2 packs the two 32-k blocks of a unit into one activation load
+// for M <= 8, as described at the AQ4 register-staged kernel; the two block
+// products accumulate separately and each lane keeps its own class's.
+template <int MT, int WAVES, int S, int B, int DEPTH, int P>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
     GemvArgs a) {
+  static_assert(P == 1 || (P == 2 && MT == 1), "row packing: one m-tile");
+  constexpr int XR = 2 / P;            // activation registers per unit
+  constexpr uint32_t RP = 16 / P;      // rows per class
   __shared__ float red[2][WAVES * S * MT * 4 * kWave];
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1145,15 +1154,17 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
   uint32_t xoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = mt * 16 + lane % 16;
-    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 16 * (lane / 16)) * 2)
+    const uint32_t m = mt * 16 + (lane % 16) % RP;
+    const uint32_t c = (lane % 16) / RP;
+    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 16 * (lane / 16)) * 2 + 16 * c)
                         : 0x80000000u;
   }
+  const uint32_t lcls = (lane / 16) * 4 / RP;
   const uint32_t wlane = lane * 16, slane = (lane % 16) * 4;
 
   struct Batch {
     u32x4 w[B][S];
-    bf16x8 x[B][MT][2];
+    bf16x8 x[B][MT][XR];
     float rs[S];
   };
   // Load pointer: stripe group lg of the run, unit lu (scalars).  Past the
@@ -1167,10 +1178,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          bt.x[i][mt][h] = __builtin_bit_cast(
+        for (int t = 0; t < XR; ++t) {
+          bt.x[i][mt][t] = __builtin_bit_cast(
               bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                          xbuf, xoff[mt], ((lu + i) * 128 + h * 16) | xpast, 0));
+                          xbuf, xoff[mt], ((lu + i) * 128 + t * 16) | xpast, 0));
         }
       }
 #pragma unroll
@@ -1197,14 +1208,20 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 #pragma unroll
   for (int r = 0; r + 1 < DEPTH; ++r) {
     issue(ring[r]);
+    // Keep the batches in ring order: the steady-state waits assume that
+    // batch r's loads are all older than batch r + 1's.
+    __builtin_amdgcn_sched_barrier(0);
   }
-  f32x4 acc[S][MT];
+  f32x4 acc[S][MT][P];
   auto zero_acc = [&]() {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        acc[s][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < P; ++c) {
+          acc[s][mt][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
   };
@@ -1226,8 +1243,9 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
             __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[s][mt] = mfma_bf16(bt.x[i][mt][0], w0, acc[s][mt]);
-          acc[s][mt] = mfma_bf16(bt.x[i][mt][1], w1, acc[s][mt]);
+          acc[s][mt][0] = mfma_bf16(bt.x[i][mt][0], w0, acc[s][mt][0]);
+          acc[s][mt][P - 1] =
+              mfma_bf16(bt.x[i][mt][XR - 1], w1, acc[s][mt][P - 1]);
         }
       }
     }
@@ -1238,9 +1256,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
       for (int s = 0; s < S; ++s) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
+          const f32x4 q = P == 1 || lcls == 0 ? acc[s][mt][0] : acc[s][mt][P - 1];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            rb[(((wave * S + s) * MT + mt) * 4 + r) * kWave + lane] = acc[s][mt][r];
+            rb[(((wave * S + s) * MT + mt) * 4 + r) * kWave + lane] = q[r];
           }
         }
       }
@@ -1248,13 +1267,18 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
       const uint32_t Tg = T0 + cgp * S;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        for (uint32_t o = threadIdx.x; o < MT * 256; o += WAVES * kWave) {
-          const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
-          const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+        for (uint32_t o = threadIdx.x; o < MT * RP * 16; o += WAVES * kWave) {
+          const uint32_t mt = o / (RP * 16), mrow = (o % (RP * 16)) / 16;
+          const uint32_t ncol = o % 16;
           float v = 0.0f;
 #pragma unroll
-          for (int w = 0; w < WAVES; ++w) {
-            v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+          for (int c = 0; c < P; ++c) {
+            const uint32_t arow = c * RP + mrow;
+            const uint32_t src = ncol + 16 * (arow / 4), r = arow % 4;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+              v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+            }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
           if (m < a.m && n < a.n) {
@@ -1290,11 +1314,28 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 // structure with 128-k groups.  Each wave reads its K share of x from L2
 // into registers once per group of S adjacent stripes; the per-group
 // activation sums come from one MFMA against a ones operand, shared by the S
-// stripes, so a group costs 4 (S + 1) MFMAs per m-tile plus the fp32
-// correction of each stripe.  Requires groups % (WAVES * B) == 0.
-template <int MT, int WAVES, int S, int B, int DEPTH>
+// stripes.  Requires groups % (WAVES * B) == 0.
+//
+// Row packing (P = 2 or 4, one m-tile, M <= 16 / P): the 16 A rows of an
+// MFMA are split into P classes of 16 / P rows, and class c of x register t
+// holds the activation rows for 32-k block P t + c of the group.  One 16-byte
+// activation load then carries P blocks instead of one, which matters
+// because the texture path charges every activation load for 64 lanes
+// whether or not their rows exist (AQ4 M=8 14336->4096 on MI355X: 12.8 us
+// with four activation loads per group, 8.3 us with one).  The product of
+// register t with block P t + c's weights is valid only in class c's rows,
+// so the P block products go to separate accumulators p[c] and each lane
+// keeps the one of its own class (a lane's four accumulator rows lie in one
+// class); the class rows of a stripe are summed in the final reduction.  The
+// ones-MFMA of register t gives every class the sum over its own blocks, so
+// a group needs 4 / P sum MFMAs instead of 4.
+template <int MT, int WAVES, int S, int B, int DEPTH, int P>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
     GemvArgs a) {
+  static_assert(P == 1 || MT == 1, "row packing needs a single m-tile");
+  static_assert(P == 1 || P == 2 || P == 4, "P divides the 4 blocks of a group");
+  constexpr int XR = 4 / P;            // activation registers per group
+  constexpr uint32_t RP = 16 / P;      // rows per class
   __shared__ float red[2][WAVES * S * MT * 4 * kWave];
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -1319,13 +1360,18 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
   const uint32_t rows = min(32u, a.m - m0);
   const __amdgpu_buffer_rsrc_t xbuf = byte_buffer(
       a.x + uint64_t(m0) * a.ldx, uint32_t(((rows - 1) * a.ldx + a.k) * 2));
+  // Lane l reads row m of its class and the 8 k of k-slot group l / 16 of
+  // its block (byte 64 c within the register's P-block span).
   uint32_t xoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = mt * 16 + lane % 16;
-    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 8 * (lane / 16)) * 2)
+    const uint32_t m = mt * 16 + (lane % 16) % RP;
+    const uint32_t c = (lane % 16) / RP;
+    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 8 * (lane / 16)) * 2 + 64 * c)
                         : 0x80000000u;
   }
+  // Class of this lane's accumulator rows 4 (l / 16) .. + 3.
+  const uint32_t lcls = (lane / 16) * 4 / RP;
   const uint32_t wlane = lane * 16, zlane = (lane % 16) * 4;
   const bf16x8 ones = __builtin_bit_cast(
       bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
@@ -1335,7 +1381,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
   struct Batch {
     u32x4 w[B][S];
     uint32_t sz[B][S];
-    bf16x8 x[B][MT][4];
+    bf16x8 x[B][MT][XR];
   };
   uint32_t lg = 0, lu = ub;
   auto issue = [&](Batch &bt) {
@@ -1345,10 +1391,11 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          bt.x[i][mt][j] = __builtin_bit_cast(
+        for (int t = 0; t < XR; ++t) {
+          bt.x[i][mt][t] = __builtin_bit_cast(
               bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                          xbuf, xoff[mt], ((lu + i) * 256 + j * 64) | xpast, 0));
+                          xbuf, xoff[mt],
+                          ((lu + i) * 256 + t * P * 64) | xpast, 0));
         }
       }
 #pragma unroll
@@ -1372,6 +1419,9 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
 #pragma unroll
   for (int r = 0; r + 1 < DEPTH; ++r) {
     issue(ring[r]);
+    // Keep the batches in ring order: the steady-state waits assume that
+    // batch r's loads are all older than batch r + 1's.
+    __builtin_amdgcn_sched_barrier(0);
   }
   f32x4 acc[S][MT];
   auto zero_acc = [&]() {
@@ -1393,32 +1443,40 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
       for (int mt = 0; mt < MT; ++mt) {
         xsum[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          xsum[mt] = mfma_bf16(bt.x[i][mt][j], ones, xsum[mt]);
+        for (int t = 0; t < XR; ++t) {
+          xsum[mt] = mfma_bf16(bt.x[i][mt][t], ones, xsum[mt]);
         }
       }
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        f32x4 p[MT];
+        f32x4 p[P][MT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          p[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < P; ++c) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            p[c][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][s][j], nmask, nmagic);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            p[mt] = mfma_bf16(bt.x[i][mt][j], bj, p[mt]);
+            p[j % P][mt] = mfma_bf16(bt.x[i][mt][j / P], bj, p[j % P][mt]);
           }
         }
         const float sf = f16_to_f32(uint16_t(bt.sz[i][s] & 0xffffu));
         const float zoff = 128.0f + f16_to_f32(uint16_t(bt.sz[i][s] >> 16));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
+          f32x4 q = p[0][mt];
+#pragma unroll
+          for (int c = 1; c < P; ++c) {
+            q = lcls == uint32_t(c) ? p[c][mt] : q;
+          }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            acc[s][mt][r] += sf * (p[mt][r] - zoff * xsum[mt][r]);
+            acc[s][mt][r] += sf * (q[r] - zoff * xsum[mt][r]);
           }
         }
       }
@@ -1440,13 +1498,20 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
       const uint32_t Tg = T0 + cgp * S;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        for (uint32_t o = threadIdx.x; o < MT * 256; o += WAVES * kWave) {
-          const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
-          const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+        // Output row mrow of the m-tile is the sum of accumulator row
+        // c RP + mrow over the classes c.
+        for (uint32_t o = threadIdx.x; o < MT * RP * 16; o += WAVES * kWave) {
+          const uint32_t mt = o / (RP * 16), mrow = (o % (RP * 16)) / 16;
+          const uint32_t ncol = o % 16;
           float v = 0.0f;
 #pragma unroll
-          for (int w = 0; w < WAVES; ++w) {
-            v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+          for (int c = 0; c < P; ++c) {
+            const uint32_t arow = c * RP + mrow;
+            const uint32_t src = ncol + 16 * (arow / 4), r = arow % 4;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+              v += rb[(((w * S + s) * MT + mt) * 4 + r) * kWave + src];
+            }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
           if (m < a.m && n < a.n) {
@@ -1778,21 +1843,39 @@ hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
   return hipGetLastError();
 }
 
-#define ULLM_RS_KERNEL(K, MT, C) K<MT, C.waves, C.s, C.batch, C.depth>
-template <int MT>
+#define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P>
+template <int MT, int P>
 hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
-  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide), *c, a, s);
-  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge), *c, a, s);
-  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK), *c, a, s);
+  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
+  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
+  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
 }
 
-template <int MT>
+template <int MT, int P>
 hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
-  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide), *c, a, s);
-  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge), *c, a, s);
-  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK), *c, a, s);
+  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
+  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
+  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+}
+
+// Row packing of the register-staged kernels: the largest P <= the cap
+// whose classes (16 / P rows) hold M, for single-stripe groups only.  With
+// groups of S >= 2 stripes the activation loads are already shared and the
+// per-group class select costs more than the saved loads (MI355X, AQ4 M=4
+// 4096->28672, groups of 4: 15.1 us unpacked, 15.2 at P = 2, 17.5 at P = 4;
+// single stripes, M=4 14336->4096: 11.4, 9.8, 8.9 us).  ULLM_GEMV_PACK sets
+// the cap (1 = no packing).
+int rs_pack(const GemvArgs &a, const RsCfg *c, bool aq4) {
+  static const int cap = env_int("ULLM_GEMV_PACK", 4);
+  if (c->s != 1) {
+    return 1;
+  }
+  if (cap >= 4 && aq4 && a.m <= 4) {
+    return 4;
+  }
+  return cap >= 2 && a.m <= 8 ? 2 : 1;
 }
 #undef ULLM_RS_KERNEL
 
@@ -1839,7 +1922,11 @@ hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
   }
   // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
   if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec) : nullptr) {
-    return two ? launch_fp8_rs<2>(a, rs, s) : launch_fp8_rs<1>(a, rs, s);
+    if (two) {
+      return launch_fp8_rs<2, 1>(a, rs, s);
+    }
+    return rs_pack(a, rs, false) == 2 ? launch_fp8_rs<1, 2>(a, rs, s)
+                                  : launch_fp8_rs<1, 1>(a, rs, s);
   }
   const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
@@ -1858,7 +1945,14 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
   if (const RsCfg *rs = plan_rs(a, vec)) {
-    return two ? launch_aq4_rs<2>(a, rs, s) : launch_aq4_rs<1>(a, rs, s);
+    if (two) {
+      return launch_aq4_rs<2, 1>(a, rs, s);
+    }
+    switch (rs_pack(a, rs, true)) {
+      case 4: return launch_aq4_rs<1, 4>(a, rs, s);
+      case 2: return launch_aq4_rs<1, 2>(a, rs, s);
+      default: return launch_aq4_rs<1, 1>(a, rs, s);
+    }
   }
   if (use_ms(a, vec, two ? 2 : 1, true)) {
     if (two) {
