@@ -141,6 +141,8 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     (7, 1000, 8192),     # AQ4 single stripes, two classes, a ragged class
     (5, 16400, 1024),    # AQ4 groups of 4 at M = 5
     (6, 65600, 1024),    # AQ4 wide configuration at M = 6
+    (8, 1000, 4096),     # AQ4 small grid: single stripes, 8 waves, packed
+    (5, 300, 2048),      # AQ4 small grid, ragged last stripe
 ])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):

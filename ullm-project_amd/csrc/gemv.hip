@@ -1711,7 +1711,9 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //   medium (>= 384 stripes): 4 waves, groups of 2; AQ4 M=32 4096->6144 11.2
 //          against 17.9 us, M=8 6.4 against 7.9 us;
 //   deep K (< 384 stripes, K >= 8192): 16 waves, single stripes; AQ4 M=8
-//          14336->4096 13.0 against 14.3 us.
+//          14336->4096 13.0 against 14.3 us (11.7 with rows packed);
+//   small  (< 384 stripes, M <= 8, rows packed): 8 waves, single stripes;
+//          AQ4 M=8 4096->4096 4.9 against 5.3 us.
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
@@ -1728,10 +1730,14 @@ struct RsCfg {
 #ifndef ULLM_RS_DEEPK
 #define ULLM_RS_DEEPK 16, 1, 2, 1
 #endif
+#ifndef ULLM_RS_SMALL
+#define ULLM_RS_SMALL 8, 1, 2, 1
+#endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
+constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
 
 // Whether the multi-stripe kernel takes this launch.  It stages the
 // activation block once per workgroup and amortises it over a run of
@@ -1821,6 +1827,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec) {
                    : stripes >= 1024 ? &kRsLarge
                    : stripes >= 384  ? &kRsMedium
                    : a.k >= 8192     ? &kRsDeepK
+                   : a.m <= 8        ? &kRsSmall
                                      : nullptr;
   if (c == nullptr && forced == 1) {
     c = &kRsMedium;
@@ -1849,7 +1856,8 @@ hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
 template <int MT, int P>
@@ -1857,7 +1865,8 @@ hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
 // Row packing of the register-staged kernels: the largest P <= the cap
