@@ -105,7 +105,8 @@ def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="aq4 gemv bf16")
 
 
-@pytest.mark.parametrize("m,n", [(1, 9000), (4, 25000), (8, 12500), (16, 12500)])
+@pytest.mark.parametrize("m,n", [(1, 9000), (2, 9000), (3, 25000), (4, 25000),
+                                 (8, 12500), (16, 12500)])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     """Enough 16-row stripes (the last one ragged) that the launcher gives each

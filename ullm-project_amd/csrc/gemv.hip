@@ -728,10 +728,14 @@ uint32_t ms_lds_bytes(const GemvArgs &a, bool aq4) {
 // not wait on vector loads (the next stripe's weights stay in flight), and
 // the sub-group's threads store.  `red` is this sub-group's buffer, `kw` the
 // wave's index within it, `live` whether the stripe exists.
-template <int MT, int KS>
+template <int MT, int KS, int P = 1, int ROWS = 16>
 __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
                                          float *red, uint32_t T, float scale,
                                          uint32_t kw, bool live) {
+  // P = 4: the four classes (lane groups l / 16) are summed in registers
+  // first, leaving every lane with the full sum of rows 0..3; only the first
+  // ROWS rows are stored.
+  static_assert(P == 1 || (P == 4 && MT == 1 && ROWS <= 4), "packing");
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t m_base = blockIdx.y * 32;
   auto store = [&](uint32_t m, uint32_t n, float v) {
@@ -744,13 +748,27 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
       }
     }
   };
-  if constexpr (KS == 1) {
+  if constexpr (P == 4) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      acc[0][r] += __shfl_xor(acc[0][r], 16, kWave);
+      acc[0][r] += __shfl_xor(acc[0][r], 32, kWave);
+    }
+  }
+  if constexpr (KS == 1 && P == 1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         store(m_base + mt * 16 + 4 * (lane / 16) + r, T * 16 + lane % 16,
               acc[mt][r]);
+      }
+    }
+  } else if constexpr (KS == 1) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      if (lane < 16) {
+        store(m_base + r, T * 16 + lane, acc[0][r]);
       }
     }
   } else {
@@ -762,9 +780,12 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
       }
     }
     lds_barrier();
-    for (uint32_t o = kw * kWave + lane; o < MT * 256; o += KS * kWave) {
-      const uint32_t mt = o / 256, mrow = (o % 256) / 16, ncol = o % 16;
-      const uint32_t src = ncol + 16 * (mrow / 4), r = mrow % 4;
+    for (uint32_t o = kw * kWave + lane; o < MT * ROWS * 16; o += KS * kWave) {
+      const uint32_t mt = o / (ROWS * 16), mrow = (o % (ROWS * 16)) / 16;
+      const uint32_t ncol = o % 16;
+      // P = 4: row mrow's class sum sits in element mrow of lanes 0..15.
+      const uint32_t src = P == 1 ? ncol + 16 * (mrow / 4) : ncol;
+      const uint32_t r = mrow % 4;
       float v = 0.0f;
 #pragma unroll
       for (int w = 0; w < KS; ++w) {
@@ -794,10 +815,20 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
 // 4..15 of the 16-row MFMA tile empty, so only elements r < NR carry results
 // and need the per-group correction).
 // Requires groups % (KS * B) == 0 (every wave's share is whole batches).
-template <int MT, int WAVES, int KS, int B, int DEPTH, int NR>
+//
+// P = 4 (M <= 4): the A operand rows are packed in four classes of four, as
+// in the register-staged kernels: class c of the single A read of a group
+// holds the activation rows for the group's 32-k block c, so one ones-MFMA
+// gives every class its block's activation sum and the per-(row, group) sums
+// need no separate pass over LDS (the pass and its barrier sat between the
+// arrival of x and the first MFMA: 0.8 us of the M=1 4096->14336 launch on
+// MI355X).  Block c's product is valid in class c's rows only; each lane
+// keeps its own class's, and the classes are summed at the stripe's end.
+template <int MT, int WAVES, int KS, int B, int DEPTH, int NR, int P>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     GemvArgs a) {
   static_assert(NR == 4 || MT == 1, "NR < 4 only for a single m-tile");
+  static_assert(P == 1 || (P == 4 && MT == 1), "row packing: one m-tile");
   static_assert(WAVES % KS == 0, "sub-groups");
   constexpr uint32_t SG = WAVES / KS;
   constexpr uint32_t RED = KS > 1 ? 2 * WAVES * MT * 4 * kWave : 1;
@@ -864,7 +895,8 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   wait_vmcnt<(DEPTH - 1) * 2 * B>();  // this thread's activation copies landed
   lds_barrier();
   // Group sums: 16 lanes per (row, group), one chunk each, then a butterfly.
-  for (uint32_t base = 0; base < rows * groups * 16; base += WAVES * kWave) {
+  for (uint32_t base = 0; P == 1 && base < rows * groups * 16;
+       base += WAVES * kWave) {
     const uint32_t i = base + threadIdx.x;
     const uint32_t item = i / 16, c = i % 16;
     float sum = 0.0f;
@@ -885,17 +917,23 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
       gsum[item] = sum;
     }
   }
-  lds_barrier();
+  if constexpr (P == 1) {
+    lds_barrier();
+  }
 
   // A operand of group g, MFMA j: chunk 16 g + 4 j + lane / 16 of the lane's
   // row, i.e. byte (16 g + 4 j) * 16 past the lane base.
+  // Packed (P = 4): lane l reads row l % 4 of class (l % 16) / 4, i.e.
+  // chunk 16 g + 4 ((l % 16) / 4) + l / 16, for the single A read of group g.
   const char *xa[MT];
   const float *gs[MT][4];  // group-sum row of each accumulator element
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = mt * 16 + lane % 16;
+    const uint32_t m = P == 1 ? mt * 16 + lane % 16 : lane % 4;
     const uint32_t r = m < rows ? m : rows;
-    xa[mt] = reinterpret_cast<const char *>(xs) + (r * pitch + lane / 16) * 16;
+    const uint32_t c0 = P == 1 ? 0u : 4u * ((lane % 16) / 4);
+    xa[mt] = reinterpret_cast<const char *>(xs) +
+             (r * pitch + c0 + lane / 16) * 16;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t mr = mt * 16 + 4 * (lane / 16) + e;
@@ -904,6 +942,10 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   }
   const uint32_t nmask = opaque_u32(0x000f000fu);
   const uint32_t nmagic = opaque_u32(0x43004300u);
+  const bf16x8 ones = __builtin_bit_cast(
+      bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+  // Class of this lane's rows (P = 4): lane / 16.
+  const bool odd = (lane / 16) & 1u, high = (lane / 32) & 1u;
 
   f32x4 acc[MT];
 #pragma unroll
@@ -912,7 +954,36 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   }
   // Consume pointer: the wave's cs-th stripe, group cg.
   uint32_t cs = 0, cg = ub;
-  auto consume = [&](const Batch &bt) {
+  auto consume_packed = [&](const Batch &bt) {
+    f32x4 xsum[B], p[B][4];
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const bf16x8 xa0 =
+          *reinterpret_cast<const bf16x8 *>(xa[0] + (cg + i) * 256);
+      xsum[i] = mfma_bf16(xa0, ones, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        p[i][c] = mfma_bf16(xa0, nib8_to_bf16_off128(bt.w[i][c], nmask, nmagic),
+                            f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B; ++i) {
+      const float sf = f16_to_f32(uint16_t(bt.sz[i] & 0xffffu));
+      const float zoff = 128.0f + f16_to_f32(uint16_t(bt.sz[i] >> 16));
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        // Two-level select on the lane's class bits, element by element (a
+        // select over the whole p[i][.] array compiled to a dynamically
+        // indexed stack copy).
+        const float q01 = odd ? p[i][1][r] : p[i][0][r];
+        const float q23 = odd ? p[i][3][r] : p[i][2][r];
+        const float q = high ? q23 : q01;
+        acc[0][r] += sf * (q - zoff * xsum[i][r]);
+      }
+    }
+  };
+  auto consume_plain = [&](const Batch &bt) {
     f32x4 p[B][MT];
 #pragma unroll
     for (int i = 0; i < B; ++i) {
@@ -947,11 +1018,19 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
         }
       }
     }
+  };
+  auto consume = [&](const Batch &bt) {
+    if constexpr (P == 4) {
+      consume_packed(bt);
+    } else {
+      consume_plain(bt);
+    }
     cg += B;
     if (cg == ue) {  // stripe done: reduce, store, reset
       const uint32_t sr = sg + cs * SG;  // run stripe
-      flush_ks<MT, KS>(a, acc, red + (cs & 1) * (RED / 2) + sg * KS * MT * 4 * kWave,
-                       T0 + sr, 1.0f, kw, sr < nS);
+      flush_ks<MT, KS, P, P == 1 ? 16 : NR>(a, acc,
+                          red + (cs & 1) * (RED / 2) + sg * KS * MT * 4 * kWave,
+                          T0 + sr, 1.0f, kw, sr < nS);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1794,11 +1873,11 @@ hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
   return launch_lds(kernel, grid, dim3(waves * kWave), lds, s, a);
 }
 
-template <int MT, int NR>
+template <int MT, int NR, int P>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
       aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch,
-                         kAq4Ms.depth, NR>,
+                         kAq4Ms.depth, NR, P>,
       a, kAq4Ms.waves, ms_lds_bytes(a, true), s, kAq4Ms.waves / kAq4Ms.ks);
 }
 
@@ -1965,11 +2044,17 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   }
   if (use_ms(a, vec, two ? 2 : 1, true)) {
     if (two) {
-      return launch_aq4_ms<2, 4>(a, s);
+      return launch_aq4_ms<2, 4, 1>(a, s);
     }
-    return a.m == 1 ? launch_aq4_ms<1, 1>(a, s)
-                    : a.m == 2 ? launch_aq4_ms<1, 2>(a, s)
-                               : launch_aq4_ms<1, 4>(a, s);
+    // Rows packed four classes deep up to M = 4 (ULLM_GEMV_PACK < 4 turns
+    // this off).
+    static const int cap = env_int("ULLM_GEMV_PACK", 4);
+    if (a.m > 4 || cap < 4) {
+      return launch_aq4_ms<1, 4, 1>(a, s);
+    }
+    return a.m == 1 ? launch_aq4_ms<1, 1, 4>(a, s)
+                    : a.m == 2 ? launch_aq4_ms<1, 2, 4>(a, s)
+                               : launch_aq4_ms<1, 4, 4>(a, s);
   }
   const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
