@@ -54,6 +54,26 @@ typedef uint32_t ullm_linear_encoding_t;
  * + f16 scale [N][K/128] + f16 zero [N][K/128]; K % 128 == 0. */
 #define ULLM_LINEAR_ENCODING_AQ4_G128 UINT32_C(2)
 
+/* Row layouts of a weight (ullm_linear_weight_desc_t.layout). */
+#define ULLM_LINEAR_LAYOUT_PLAIN UINT32_C(0)
+/* A fused gate/up projection: N = 2F rows, the F gate rows followed by the F
+ * up rows of the same output features.  The library stores each feature's
+ * gate and up rows side by side so that a forward with
+ * ULLM_LINEAR_EPILOGUE_SILU_MUL produces Y[M][F] = silu(X Wg^T) * (X Wu^T)
+ * in one pass.  Export and dequantize still use the canonical [2F][K] order. */
+#define ULLM_LINEAR_LAYOUT_GATED_PAIRS UINT32_C(1)
+
+/* Output epilogues (ullm_linear_forward_desc_t.epilogue), applied in fp32
+ * after alpha, before the output is rounded. */
+#define ULLM_LINEAR_EPILOGUE_NONE UINT32_C(0)
+/* Gated-pair weight only: Y[m][j] = silu(a*g) * (a*u), g and u the gate and
+ * up products of feature j, a = alpha, silu(v) = v / (1 + exp(-v)).  Y has
+ * F = N / 2 columns. */
+#define ULLM_LINEAR_EPILOGUE_SILU_MUL UINT32_C(1)
+/* Y = alpha * X W^T + R for a residual R [M][N] (bf16 or f32).  R may be Y
+ * itself (same pointer, dtype and row stride): an in-place residual add. */
+#define ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD UINT32_C(2)
+
 /* What ullm_linear_weight_desc_t.values holds. */
 #define ULLM_LINEAR_SOURCE_F32 UINT32_C(1)     /* f32 [N][K], quantized here */
 #define ULLM_LINEAR_SOURCE_ENCODED UINT32_C(2) /* already-encoded buffers */
@@ -91,7 +111,9 @@ typedef struct ullm_linear_weight_desc_t {
   const void *scales; /* ENCODED only */
   const void *zeros;  /* ENCODED AQ4 only */
   void *stream;       /* upload/quantize stream; creation blocks until done */
-  uint64_t reserved[4];
+  uint32_t layout;    /* ULLM_LINEAR_LAYOUT_* (0 = plain) */
+  uint32_t reserved0;
+  uint64_t reserved[3];
 } ullm_linear_weight_desc_t;
 
 typedef struct ullm_linear_weight_info_t {
@@ -102,7 +124,9 @@ typedef struct ullm_linear_weight_info_t {
   uint64_t n;
   uint64_t k;
   uint64_t device_bytes; /* bytes the weight holds in HBM */
-  uint64_t reserved[4];
+  uint32_t layout;       /* ULLM_LINEAR_LAYOUT_* */
+  uint32_t reserved0;
+  uint64_t reserved[3];
 } ullm_linear_weight_info_t;
 
 typedef struct ullm_linear_forward_desc_t {
@@ -122,7 +146,11 @@ typedef struct ullm_linear_forward_desc_t {
   void *stream;
   void *workspace; /* device scratch for ACT_FP8_PER_TOKEN; null = library-owned */
   uint64_t workspace_size;
-  uint64_t reserved[4];
+  uint32_t epilogue;            /* ULLM_LINEAR_EPILOGUE_* (0 = none) */
+  uint32_t residual_dtype;      /* RESIDUAL_ADD: BF16 or F32 */
+  const void *residual;         /* RESIDUAL_ADD: device [M][residual_row_stride] */
+  uint64_t residual_row_stride; /* elements, 0 = N */
+  uint64_t reserved[1];
 } ullm_linear_forward_desc_t;
 
 typedef struct ullm_linear_act_quant_desc_t {
@@ -182,7 +210,9 @@ ULLM_HIP_API ullm_status_t ullm_linear_weight_dequantize(
     const ullm_linear_weight_t *weight, float *out, void *stream,
     ullm_error_sink_t *error_sink);
 
-/* Y = alpha * X * W^T.  Stream-ordered. */
+/* Y = alpha * X * W^T, then the descriptor's epilogue.  Stream-ordered.
+ * A gated-pair weight requires ULLM_LINEAR_EPILOGUE_SILU_MUL (its Y has N / 2
+ * columns); SILU_MUL requires a gated-pair weight. */
 ULLM_HIP_API ullm_status_t ullm_linear_forward(
     const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink);
 

@@ -64,6 +64,7 @@ def lib() -> ctypes.CDLL:
             "orc_aq4_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
             "orc_act_quantize": (None, [_I, _I, _P, _I, _P, _P]),
             "orc_fp8_gemm": (None, [_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
+            "orc_silu_mul": (None, [_I, _I, _P, _P]),
             "orc_max_threads": (ctypes.c_int, []),
         }
         for name, (res, args) in sig.items():
@@ -212,6 +213,16 @@ def fp8_gemm(xq, xs, q, s, alpha=1.0, want64=False, threads=0):
     lib().orc_fp8_gemm(m, n, k, _p(xq), _p(xs), _p(q), _p(s), alpha,
                        _p(y32), _p(y64), threads)
     return y32, y64
+
+
+def silu_mul(gu):
+    """SiLU-gate epilogue of an fp32 gate/up product gu [m][2F] -> [m][F]."""
+    gu = np.ascontiguousarray(gu, np.float32)
+    m, f2 = gu.shape
+    assert f2 % 2 == 0
+    out = np.empty((m, f2 // 2), np.float32)
+    lib().orc_silu_mul(m, f2 // 2, _p(gu), _p(out))
+    return out
 
 
 def max_threads() -> int:

@@ -415,3 +415,15 @@ void orc_fp8_gemm(int64_t m, int64_t n, int64_t k, const uint8_t *xq,
     }
   }
 }
+
+/* SiLU-gate epilogue: gate columns [0, f), up columns [f, 2f) of each row. */
+void orc_silu_mul(int64_t m, int64_t f, const float *gu, float *out) {
+  for (int64_t i = 0; i < m; ++i) {
+    for (int64_t j = 0; j < f; ++j) {
+      const float g = gu[i * 2 * f + j];
+      const float u = gu[i * 2 * f + f + j];
+      const float silu = g / (1.0f + expf(-g));
+      out[i * f + j] = silu * u;
+    }
+  }
+}

@@ -34,6 +34,14 @@
  *                     fp32 accumulation in increasing k.  AQ4 uses Wd.
  *   act quant         a_m = max_k |x[m,k]| / 448; XA = e4m3(x / a_m); a_m == 0 -> XA = 0.
  *   FP8 GEMM          Y32[m,n] = alpha * ((a_m * s_n) * sum_k e4m3(XA) * e4m3(Q)).
+ *   SiLU-gate epilogue  for a fused gate/up product Y32[m][2F] (gate columns
+ *                     0..F-1, up columns F..2F-1, alpha already applied):
+ *                     out[m,j] = silu(Y32[m,j]) * Y32[m,F+j],
+ *                     silu(v) = v / (1 + expf(-v))  (fp32, libm expf).
+ *                     No reference file defines it: the survey lists the fused
+ *                     SiLU-gate epilogue as the path's next step, and this is
+ *                     the standard SwiGLU gate (x * sigmoid(x)).
+ *   residual epilogue Y32 + R, one fp32 add per element.
  *
  * All functions take row strides in elements where a caller may hand a view.
  */
@@ -89,6 +97,9 @@ void orc_act_quantize(int64_t m, int64_t k, const uint16_t *x, int64_t ldx,
 void orc_fp8_gemm(int64_t m, int64_t n, int64_t k, const uint8_t *xq,
                   const float *xs, const uint8_t *q, const float *s,
                   float alpha, float *y32, double *y64, int threads);
+
+/* epilogues on an fp32 product (see the definitions above) */
+void orc_silu_mul(int64_t m, int64_t f, const float *gu, float *out);
 
 /* number of OpenMP threads the library would use for threads <= 0 */
 int orc_max_threads(void);

@@ -55,11 +55,15 @@ int main(void) {
   S(ullm_backend_probe_result_t) F(ullm_backend_probe_result_t, hip_runtime_present)
   S(ullm_context_probe_result_t) F(ullm_context_probe_result_t, reserved)
   S(ullm_linear_weight_desc_t) F(ullm_linear_weight_desc_t, n) F(ullm_linear_weight_desc_t, memory)
-  F(ullm_linear_weight_desc_t, values) F(ullm_linear_weight_desc_t, stream) F(ullm_linear_weight_desc_t, reserved)
-  S(ullm_linear_weight_info_t) F(ullm_linear_weight_info_t, device_bytes) F(ullm_linear_weight_info_t, reserved)
+  F(ullm_linear_weight_desc_t, values) F(ullm_linear_weight_desc_t, stream) F(ullm_linear_weight_desc_t, layout)
+  F(ullm_linear_weight_desc_t, reserved0) F(ullm_linear_weight_desc_t, reserved)
+  S(ullm_linear_weight_info_t) F(ullm_linear_weight_info_t, device_bytes) F(ullm_linear_weight_info_t, layout)
+  F(ullm_linear_weight_info_t, reserved)
   S(ullm_linear_forward_desc_t) F(ullm_linear_forward_desc_t, m) F(ullm_linear_forward_desc_t, x_scales)
   F(ullm_linear_forward_desc_t, y_row_stride) F(ullm_linear_forward_desc_t, x_dtype) F(ullm_linear_forward_desc_t, alpha)
-  F(ullm_linear_forward_desc_t, stream) F(ullm_linear_forward_desc_t, workspace_size) F(ullm_linear_forward_desc_t, reserved)
+  F(ullm_linear_forward_desc_t, stream) F(ullm_linear_forward_desc_t, workspace_size) F(ullm_linear_forward_desc_t, epilogue)
+  F(ullm_linear_forward_desc_t, residual_dtype) F(ullm_linear_forward_desc_t, residual)
+  F(ullm_linear_forward_desc_t, residual_row_stride) F(ullm_linear_forward_desc_t, reserved)
   S(ullm_linear_act_quant_desc_t) F(ullm_linear_act_quant_desc_t, xq) F(ullm_linear_act_quant_desc_t, reserved)
   S(ullm_linear_weight_export_desc_t) F(ullm_linear_weight_export_desc_t, values) F(ullm_linear_weight_export_desc_t, reserved)
   return 0;
@@ -221,7 +225,10 @@ def _wdesc(uh, **kw):
 @pytest.mark.parametrize("change,status", [
     (dict(struct_size=8), "INVALID_ARGUMENT"),
     (dict(abi_version=7), "INVALID_ABI_VERSION"),
-    (dict(reserved=(0, 0, 1, 0)), "RESERVED_NONZERO"),
+    (dict(reserved=(0, 0, 1)), "RESERVED_NONZERO"),
+    (dict(reserved0=1), "RESERVED_NONZERO"),
+    (dict(layout=7), "INVALID_ARGUMENT"),
+    (dict(layout=1, n=15), "INVALID_ARGUMENT"),     # gated pair needs even N
     (dict(encoding=9), "UNSUPPORTED"),
     (dict(source=0), "INVALID_ARGUMENT"),
     (dict(memory=5), "INVALID_ARGUMENT"),
@@ -261,7 +268,7 @@ def test_linear_entry_points_reject_bad_handles(uh):
     assert lib.ullm_linear_forward(ctypes.byref(fwd), None) == uh.Status.INVALID_ARGUMENT
     assert lib.ullm_linear_forward(None, None) == uh.Status.INVALID_ARGUMENT
     fwd = uh.new(uh.ForwardDesc, weight=bogus)
-    fwd.reserved[3] = 1
+    fwd.reserved[0] = 1
     assert lib.ullm_linear_forward(ctypes.byref(fwd), None) == uh.Status.RESERVED_NONZERO
     h = ctypes.c_void_p(0x1234)
     assert lib.ullm_linear_weight_destroy(ctypes.byref(h), None) == uh.Status.HIP_INVALID_HANDLE

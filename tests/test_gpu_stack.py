@@ -1,7 +1,8 @@
 """GPU parity of the decode-stack driver (ullm-project_amd/stack.py) on a
 scaled-down stack: every projection of the chain, including the strided
-pass-through views and the per-layer alpha, is checked against the oracle
-applied to the GPU's own input of that projection (1e-2 x RMS each)."""
+pass-through view, the SiLU-gated gate_up and the per-layer alpha, is checked
+against the oracle applied to the GPU's own input of that projection
+(1e-2 x RMS each)."""
 import math
 
 import numpy as np
@@ -13,7 +14,8 @@ from helpers import assert_close
 pytestmark = pytest.mark.gpu
 
 
-def test_small_stack_chain(uh, orc, gpu):
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_small_stack_chain(uh, orc, gpu, swiglu):
     import stack
     hidden, qkv, ffn, vocab, layers = 256, 384, 512, 1000, 2
     rs = np.random.default_rng(3)
@@ -23,20 +25,23 @@ def test_small_stack_chain(uh, orc, gpu):
     weights = {i: w for i, w in enumerate(wts)}
     weights["lm_head"] = lm
     st = stack.DecodeStack(uh, torch, gpu, batch=8, layers=layers, hidden=hidden,
-                           qkv=qkv, ffn=ffn, vocab=vocab, weights=weights)
+                           qkv=qkv, ffn=ffn, vocab=vocab, weights=weights,
+                           swiglu=swiglu)
     st.h0.copy_(torch.from_numpy(rs.standard_normal((8, hidden)).astype(np.float32)).to(gpu))
     st.h.copy_(st.h0)
 
     def bits(t):
         return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
-    def check(w_f32, x_bits, y_gpu, alpha):
+    def check(w_f32, x_bits, y_gpu, alpha, gated=False):
         p, s, z = orc.aq4_quantize(w_f32.cpu().numpy())
         ref, _ = orc.aq4_gemv(np.ascontiguousarray(x_bits), p, s, z, alpha=alpha)
+        if gated:
+            ref = orc.silu_mul(ref)
         assert_close(y_gpu.float().cpu().numpy(), ref, bf16_out=True, what="stack")
 
     a_h = 1 / (0.02 * math.sqrt(hidden))
-    a_f = 1 / (0.02 * math.sqrt(ffn))
+    a_f = 1 / (0.02 * math.sqrt(ffn) * (stack.SILU_RMS if swiglu else 1.0))
     for layer in range(layers):
         w = st.weights[layer]
         x0 = bits(st.h)
@@ -46,10 +51,10 @@ def test_small_stack_chain(uh, orc, gpu):
         w["o"].forward(st.qkv_out[:, :hidden], st.o_out, alpha=st.alpha_h)
         check(wts[layer]["o"], x1, st.o_out, a_h)
         x2 = bits(st.o_out)
-        w["gate_up"].forward(st.o_out, st.gu_out, alpha=st.alpha_h)
-        check(wts[layer]["gate_up"], x2, st.gu_out, a_h)
-        x3 = bits(st.gu_out)[:, :ffn]
-        w["down"].forward(st.gu_out[:, :ffn], st.h, alpha=st.alpha_f)
+        w["gate_up"].forward(st.o_out, st.act, alpha=st.alpha_h)
+        check(wts[layer]["gate_up"], x2, st.act, a_h, gated=swiglu)
+        x3 = bits(st.act)[:, :ffn]
+        w["down"].forward(st.act[:, :ffn], st.h, alpha=st.alpha_f)
         check(wts[layer]["down"], x3, st.h, a_f)
     x4 = bits(st.h)
     st.lm_head.forward(st.h, st.logits, alpha=st.alpha_h)

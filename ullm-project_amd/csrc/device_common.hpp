@@ -166,4 +166,60 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t byte_buffer(const void *p,
 }
 constexpr int kNt = 2;                      // nontemporal cache policy bit
 
+// ------------------------------------------------------------ epilogues
+// What the linear kernels do with an output element after alpha is applied.
+enum : uint32_t {
+  kEpiNone = 0,      // y = v
+  kEpiSiluMul = 1,   // gated-pair weight: y[:, j] = silu(gate_j) * up_j
+  kEpiResidual = 2,  // y = v + r (r may be y itself)
+};
+struct Epilogue {
+  uint32_t kind;
+  uint32_t n_out;    // output columns: N, or F = N / 2 for kEpiSiluMul
+  const void *res;   // kEpiResidual: r [m][ldr], bf16 or f32
+  uint64_t ldr;
+  bool res_f32;
+};
+
+// silu(g) = g * sigmoid(g) = g / (1 + e^-g), in fp32.
+__device__ __forceinline__ float silu_f32(float g) {
+  return g / (1.0f + expf(-g));
+}
+
+// Store output element (m, p): p is the column in the weight's physical row
+// order (its tile layout), n the weight's logical row count, v the value
+// with alpha applied, ok whether row m exists (and the column's stripe is
+// live).  Every lane of a wave must reach this call in the same control flow
+// with its own (m, p) and the (m, p ^ 8) partner in lane ^ 8, as the MFMA
+// output layout places them: kEpiSiluMul takes the up product from there.
+// EPI is the epilogue kind, a compile-time constant so that the plain
+// kernels carry no epilogue code (it sits inside their streaming loops).
+template <uint32_t EPI>
+__device__ __forceinline__ void store_out(void *y, uint64_t ldy, bool y_f32,
+                                          const Epilogue &e, uint32_t n,
+                                          uint32_t m, uint32_t p, float v,
+                                          bool ok) {
+  uint32_t col = p;
+  if constexpr (EPI == kEpiSiluMul) {
+    const float up = __shfl_xor(v, 8, kWave);
+    col = (p / 16) * 8 + p % 16;
+    ok = ok && p % 16 < 8 && col < e.n_out;
+    v = silu_f32(v) * up;
+  } else {
+    ok = ok && p < n;
+    if (EPI == kEpiResidual && ok) {
+      const uint64_t i = uint64_t(m) * e.ldr + p;
+      v += e.res_f32 ? static_cast<const float *>(e.res)[i]
+                     : bf16_to_f32(static_cast<const uint16_t *>(e.res)[i]);
+    }
+  }
+  if (ok) {
+    if (y_f32) {
+      static_cast<float *>(y)[uint64_t(m) * ldy + col] = v;
+    } else {
+      static_cast<uint16_t *>(y)[uint64_t(m) * ldy + col] = f32_to_bf16(v);
+    }
+  }
+}
+
 }  // namespace ullm

@@ -56,9 +56,11 @@ struct GemmArgs {
   float alpha;
   bool y_f32;
   bool y_vec;  // bf16 rows 16-byte aligned: coalesced epilogue stores
+  Epilogue epi;
 };
 
 // 256 threads, block tile 64 (m) x 64 (n); wave (wm, wn) owns 32 x 32.
+template <uint32_t EPI>
 __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
                                                               bool vec) {
   const int lane = threadIdx.x % kWave;
@@ -101,14 +103,10 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
       const uint32_t n = (T0 + j) * 16 + lane % 16;
       for (int r = 0; r < 4; ++r) {
         const uint32_t m = m0 + i * 16 + 4 * (lane / 16) + r;
-        if (m < a.m && n < a.n) {
-          const float v = a.alpha * ((a.xs[m] * a.scales[n]) * acc[i][j][r]);
-          if (a.y_f32) {
-            static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-          } else {
-            static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
-          }
-        }
+        const uint32_t mc = m < a.m ? m : a.m - 1;
+        const uint32_t nc = n < stripes * 16 ? n : stripes * 16 - 1;
+        const float v = a.alpha * ((a.xs[mc] * a.scales[nc]) * acc[i][j][r]);
+        store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, v, m < a.m);
       }
     }
   }
@@ -204,7 +202,7 @@ __device__ __forceinline__ i32x8 lds_operand(const char *p) {
   return __builtin_bit_cast(i32x8, v);
 }
 
-template <class C>
+template <class C, uint32_t EPI>
 __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -366,25 +364,45 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   if (!a.y_f32 && a.y_vec) {
     // bf16 out through LDS: scale, round and stage the tile, then write
     // whole 16-byte row segments.  The main loop ended on a barrier, so the
-    // operand stages are free.
+    // operand stages are free.  SiLU-gated output keeps 8 of every 16
+    // columns (gate lanes, with the up value from lane ^ 8), so its staged
+    // rows are half as wide.
     uint16_t *tile_out = reinterpret_cast<uint16_t *>(lds) +
                          wave * C::TM * 16 * C::OUT_STRIDE;
+    constexpr bool gated = EPI == kEpiSiluMul;
+    constexpr bool resid = EPI == kEpiResidual;
 #pragma unroll
     for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
         for (uint32_t j = 0; j < C::TN; ++j) {
-          const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
-          tile_out[(i * 16 + rq + r) * C::OUT_STRIDE + j * 16 + ncol] =
-              f32_to_bf16(v);
+          float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
+          uint16_t *dst = tile_out + (i * 16 + rq + r) * C::OUT_STRIDE;
+          if constexpr (gated) {
+            const float up = __shfl_xor(v, 8, kWave);
+            if (ncol < 8) {
+              dst[j * 8 + ncol] = f32_to_bf16(silu_f32(v) * up);
+            }
+          } else {
+            const uint32_t m = mw + i * 16 + rq + r, n = nw + j * 16 + ncol;
+            if (resid && m < a.m && n < a.n) {
+              const uint64_t ri = uint64_t(m) * a.epi.ldr + n;
+              v += a.epi.res_f32
+                       ? static_cast<const float *>(a.epi.res)[ri]
+                       : bf16_to_f32(static_cast<const uint16_t *>(a.epi.res)[ri]);
+            }
+            dst[j * 16 + ncol] = f32_to_bf16(v);
+          }
         }
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
-    // 16-byte segments: TN * 2 per row of the wave's tile, spread over the
-    // lanes row-major.
-    constexpr uint32_t lpr = C::TN * 2, segs = C::TM * 16 * lpr;
+    // 16-byte segments: TN * 2 per row of the wave's tile (TN gated), spread
+    // over the lanes row-major.
+    constexpr uint32_t lpr = gated ? C::TN : C::TN * 2, segs = C::TM * 16 * lpr;
+    const uint32_t n0 = gated ? nw / 2 : nw;
+    const uint32_t nlim = gated ? a.epi.n_out : a.n;
 #pragma unroll
     for (uint32_t it = 0; it < (segs + kWave - 1) / kWave; ++it) {
       const uint32_t seg = it * kWave + lane;
@@ -392,16 +410,16 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         break;
       }
       const uint32_t row = seg / lpr, c8 = (seg % lpr) * 8;
-      const uint32_t m = mw + row, n = nw + c8;
+      const uint32_t m = mw + row, n = n0 + c8;
       const u32x4 v = *reinterpret_cast<const u32x4 *>(
           tile_out + row * C::OUT_STRIDE + c8);
       uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
       if (m < a.m) {
-        if (n + 8 <= a.n) {
+        if (n + 8 <= nlim) {
           *reinterpret_cast<u32x4 *>(dst) = v;
         } else {
           const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-          for (uint32_t e = 0; e < 8 && n + e < a.n; ++e) {
+          for (uint32_t e = 0; e < 8 && n + e < nlim; ++e) {
             dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e % 2)));
           }
         }
@@ -409,7 +427,6 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     }
     return;
   }
-  const bool full = mw + C::TM * 16 <= a.m && nw + C::TN * 16 <= a.n;
 #pragma unroll
   for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
@@ -419,14 +436,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       for (uint32_t j = 0; j < C::TN; ++j) {
         const uint32_t n = nw + j * 16 + ncol;
         const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
-        if (full || (m < a.m && n < a.n)) {
-          if (a.y_f32) {
-            static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-          } else {
-            static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
-                f32_to_bf16(v);
-          }
-        }
+        store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, v, m < a.m);
       }
     }
   }
@@ -470,17 +480,17 @@ bool gemm_use_narrow(uint32_t m, uint32_t n) {
   return cost224 < cost256;
 }
 
-template <class C>
+template <class C, uint32_t EPI>
 hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C>),
+      reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(C::LDS));
   if (attr != hipSuccess) {
     return attr;
   }
   const uint32_t tiles =
       ((a.m + C::BM - 1) / C::BM) * ((a.n + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL(fp8_gemm_lds_kernel<C>, dim3(tiles), dim3(C::WAVES * kWave),
+  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(tiles), dim3(C::WAVES * kWave),
                      C::LDS, s, a);
   return hipGetLastError();
 }
@@ -494,12 +504,27 @@ bool gemm_mid_forced() {
   return v;
 }
 
+// The epilogue kind is a template parameter of the kernels.
+template <uint32_t EPI>
+hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
+                  hipStream_t s) {
+  if (vec && offsets_fit && a.k % 128 == 0 && a.m >= 128) {
+    return gemm_mid_forced() ? launch_gemm_lds<GemmMid, EPI>(a, s)
+                             : gemm_use_narrow(a.m, a.n)
+                                   ? launch_gemm_lds<GemmNarrow, EPI>(a, s)
+                                   : launch_gemm_lds<GemmLarge, EPI>(a, s);
+  }
+  const dim3 grid((a.n + 63) / 64, (a.m + 63) / 64);
+  hipLaunchKernelGGL(fp8_gemm_direct_kernel<EPI>, grid, dim3(256), 0, s, a, vec);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            const ullm_linear_weight_t *w, uint32_t m, void *y,
                            uint64_t ldy, bool y_f32, float alpha,
-                           hipStream_t s) {
+                           const Epilogue &epi, hipStream_t s) {
   GemmArgs a{};
   a.xq = xq;
   a.xs = xs;
@@ -515,18 +540,15 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   a.alpha = alpha;
   a.y_f32 = y_f32;
   a.y_vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && ldy % 8 == 0;
+  a.epi = epi;
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
   const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
                            w->fp8.bytes() < (uint64_t(1) << 32);
-  if (vec && offsets_fit && a.k % 128 == 0 && m >= 128) {
-    return gemm_mid_forced() ? launch_gemm_lds<GemmMid>(a, s)
-                             : gemm_use_narrow(m, a.n)
-                                   ? launch_gemm_lds<GemmNarrow>(a, s)
-                                   : launch_gemm_lds<GemmLarge>(a, s);
+  switch (epi.kind) {
+    case kEpiSiluMul: return gemm_e<kEpiSiluMul>(a, vec, offsets_fit, s);
+    case kEpiResidual: return gemm_e<kEpiResidual>(a, vec, offsets_fit, s);
+    default: return gemm_e<kEpiNone>(a, vec, offsets_fit, s);
   }
-  const dim3 grid((a.n + 63) / 64, (m + 63) / 64);
-  hipLaunchKernelGGL(fp8_gemm_direct_kernel, grid, dim3(256), 0, s, a, vec);
-  return hipGetLastError();
 }
 
 }  // namespace ullm

@@ -77,7 +77,7 @@ struct XRow {
   }
 };
 
-template <int MT, int WAVES>
+template <int MT, int WAVES, int EPI = kEpiNone>
 __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
                                                  f32x4 (&acc)[MT], float *red,
                                                  float scale) {
@@ -106,14 +106,8 @@ __device__ __forceinline__ void reduce_and_store(const GemvArgs &a,
     }
     const uint32_t m = m_base + mt * 16 + mrow;
     const uint32_t n = T * 16 + ncol;
-    if (m < a.m && n < a.n) {
-      v = a.alpha * (scale * v);
-      if (a.y_f32) {
-        static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-      } else {
-        static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
-      }
-    }
+    store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * (scale * v),
+              m < a.m);
   }
 }
 
@@ -125,7 +119,7 @@ constexpr int fp8_batch() { return MT == 1 ? 8 : 4; }
 template <int MT>
 constexpr int aq4_batch() { return MT == 1 ? 4 : 2; }
 
-template <int MT, int WAVES, bool VEC>
+template <int MT, int WAVES, bool VEC, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_kernel(GemvArgs a) {
   constexpr int B = fp8_batch<MT>();
   __shared__ float red[WAVES * MT * 4 * kWave];
@@ -203,10 +197,10 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_kernel(GemvArgs a) {
                 reinterpret_cast<const u32x4 *>(stripe + uint64_t(u) * 1024)),
             xa);
   }
-  reduce_and_store<MT, WAVES>(a, acc, red, rscale);
+  reduce_and_store<MT, WAVES, EPI>(a, acc, red, rscale);
 }
 
-template <int MT, int WAVES, bool VEC>
+template <int MT, int WAVES, bool VEC, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a) {
   constexpr int B = aq4_batch<MT>();
   __shared__ float red[WAVES * MT * 4 * kWave];
@@ -294,7 +288,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_kernel(GemvArgs a) {
                 reinterpret_cast<const u32x4 *>(stripe + uint64_t(g) * 256)),
             szv, xa);
   }
-  reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
+  reduce_and_store<MT, WAVES, EPI>(a, acc, red, 1.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -374,7 +368,7 @@ __device__ __forceinline__ void stage_x_lds(const GemvArgs &a, uint16_t *xs,
   }
 }
 
-template <int MT, int WAVES, int B, bool FULL>
+template <int MT, int WAVES, int B, bool FULL, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_lds_kernel(
     GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -484,14 +478,14 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_lds_kernel(
   for (int mt = 0; mt < MT; ++mt) {
     acc[mt] = (acc4[0][mt] + acc4[1][mt]) + (acc4[2][mt] + acc4[3][mt]);
   }
-  reduce_and_store<MT, WAVES>(a, acc, red, rscale);
+  reduce_and_store<MT, WAVES, EPI>(a, acc, red, rscale);
 }
 
 // AQ4: the per-(row, group) activation sums sum_k x[m, k] over each 128-k
 // group are formed once per workgroup in LDS, so each group costs four MFMAs
 // plus one fp32 correction:
 //   acc += s * (sum_k (128 + q) x  -  (128 + z) * sum_k x).
-template <int MT, int WAVES, int B, bool FULL>
+template <int MT, int WAVES, int B, bool FULL, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
     GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -638,14 +632,14 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_lds_kernel(
       }
     }
   }
-  reduce_and_store<MT, WAVES>(a, acc, red, 1.0f);
+  reduce_and_store<MT, WAVES, EPI>(a, acc, red, 1.0f);
 }
 
 // Cross-wave reduction of one stripe for the multi-stripe kernels: like
 // reduce_and_store, but for stripe T, through one of two LDS buffers that
 // alternate between stripes, and behind a barrier that leaves the weight
 // loads already issued for the next stripe in flight.
-template <int MT, int WAVES>
+template <int MT, int WAVES, int EPI = kEpiNone>
 __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
                                              f32x4 (&acc)[MT], float *red,
                                              uint32_t T, float scale) {
@@ -673,14 +667,8 @@ __device__ __forceinline__ void flush_stripe(const GemvArgs &a,
     }
     const uint32_t m = m_base + mt * 16 + mrow;
     const uint32_t n = T * 16 + ncol;
-    if (m < a.m && n < a.n) {
-      v = a.alpha * (scale * v);
-      if (a.y_f32) {
-        static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-      } else {
-        static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
-      }
-    }
+    store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * (scale * v),
+              m < a.m);
   }
 }
 
@@ -728,7 +716,7 @@ uint32_t ms_lds_bytes(const GemvArgs &a, bool aq4) {
 // not wait on vector loads (the next stripe's weights stay in flight), and
 // the sub-group's threads store.  `red` is this sub-group's buffer, `kw` the
 // wave's index within it, `live` whether the stripe exists.
-template <int MT, int KS, int P = 1, int ROWS = 16>
+template <int MT, int KS, int P = 1, int ROWS = 16, int EPI = kEpiNone>
 __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
                                          float *red, uint32_t T, float scale,
                                          uint32_t kw, bool live) {
@@ -738,15 +726,10 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
   static_assert(P == 1 || (P == 4 && MT == 1 && ROWS <= 4), "packing");
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t m_base = blockIdx.y * 32;
-  auto store = [&](uint32_t m, uint32_t n, float v) {
-    if (live && m < a.m && n < a.n) {
-      v = a.alpha * (scale * v);
-      if (a.y_f32) {
-        static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-      } else {
-        static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] = f32_to_bf16(v);
-      }
-    }
+  // Called by every lane of the wave (the epilogue pairs lanes l, l ^ 8).
+  auto store = [&](uint32_t m, uint32_t n, float v, bool ok) {
+    store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * (scale * v),
+              ok && live && m < a.m);
   };
   if constexpr (P == 4) {
 #pragma unroll
@@ -761,15 +744,14 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         store(m_base + mt * 16 + 4 * (lane / 16) + r, T * 16 + lane % 16,
-              acc[mt][r]);
+              acc[mt][r], true);
       }
     }
   } else if constexpr (KS == 1) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-      if (lane < 16) {
-        store(m_base + r, T * 16 + lane, acc[0][r]);
-      }
+      // Every lane holds the class sum; lanes 0..15 store it.
+      store(m_base + r, T * 16 + lane % 16, acc[0][r], lane < 16);
     }
   } else {
 #pragma unroll
@@ -791,7 +773,7 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
       for (int w = 0; w < KS; ++w) {
         v += red[((w * MT + mt) * 4 + r) * kWave + src];
       }
-      store(m_base + mt * 16 + mrow, T * 16 + ncol, v);
+      store(m_base + mt * 16 + mrow, T * 16 + ncol, v, true);
     }
   }
 }
@@ -824,7 +806,7 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
 // arrival of x and the first MFMA: 0.8 us of the M=1 4096->14336 launch on
 // MI355X).  Block c's product is valid in class c's rows only; each lane
 // keeps its own class's, and the classes are summed at the stripe's end.
-template <int MT, int WAVES, int KS, int B, int DEPTH, int NR, int P>
+template <int MT, int WAVES, int KS, int B, int DEPTH, int NR, int P, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     GemvArgs a) {
   static_assert(NR == 4 || MT == 1, "NR < 4 only for a single m-tile");
@@ -1028,7 +1010,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     cg += B;
     if (cg == ue) {  // stripe done: reduce, store, reset
       const uint32_t sr = sg + cs * SG;  // run stripe
-      flush_ks<MT, KS, P, P == 1 ? 16 : NR>(a, acc,
+      flush_ks<MT, KS, P, P == 1 ? 16 : NR, EPI>(a, acc,
                           red + (cs & 1) * (RED / 2) + sg * KS * MT * 4 * kWave,
                           T0 + sr, 1.0f, kw, sr < nS);
 #pragma unroll
@@ -1059,7 +1041,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
 // pipeline per wave over the run) with 64-k FP8 units.  Each batch also
 // carries the row scales of its stripe, applied once in the per-stripe
 // reduction.  Requires units % (WAVES * B) == 0.
-template <int MT, int WAVES, int B, int DEPTH>
+template <int MT, int WAVES, int B, int DEPTH, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
     GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -1170,7 +1152,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
       for (int mt = 0; mt < MT; ++mt) {
         acc[mt] = (acc4[0][mt] + acc4[1][mt]) + (acc4[2][mt] + acc4[3][mt]);
       }
-      flush_stripe<MT, WAVES>(a, acc, red[cs & 1], T0 + cs, bt.rs);
+      flush_stripe<MT, WAVES, EPI>(a, acc, red[cs & 1], T0 + cs, bt.rs);
       zero_acc();
       cu = ub;
       ++cs;
@@ -1201,7 +1183,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 // == 0.  P = 2 packs the two 32-k blocks of a unit into one activation load
 // for M <= 8, as described at the AQ4 register-staged kernel; the two block
 // products accumulate separately and each lane keeps its own class's.
-template <int MT, int WAVES, int S, int B, int DEPTH, int P>
+template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
     GemvArgs a) {
   static_assert(P == 1 || (P == 2 && MT == 1), "row packing: one m-tile");
@@ -1360,15 +1342,8 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
             }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
-          if (m < a.m && n < a.n) {
-            v = a.alpha * (bt.rs[s] * v);
-            if (a.y_f32) {
-              static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-            } else {
-              static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
-                  f32_to_bf16(v);
-            }
-          }
+          store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n,
+                    a.alpha * (bt.rs[s] * v), m < a.m);
         }
       }
       zero_acc();
@@ -1408,7 +1383,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 // class); the class rows of a stripe are summed in the final reduction.  The
 // ones-MFMA of register t gives every class the sum over its own blocks, so
 // a group needs 4 / P sum MFMAs instead of 4.
-template <int MT, int WAVES, int S, int B, int DEPTH, int P>
+template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
     GemvArgs a) {
   static_assert(P == 1 || MT == 1, "row packing needs a single m-tile");
@@ -1593,15 +1568,8 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
             }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
-          if (m < a.m && n < a.n) {
-            v = a.alpha * v;
-            if (a.y_f32) {
-              static_cast<float *>(a.y)[uint64_t(m) * a.ldy + n] = v;
-            } else {
-              static_cast<uint16_t *>(a.y)[uint64_t(m) * a.ldy + n] =
-                  f32_to_bf16(v);
-            }
-          }
+          store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * v,
+                    m < a.m);
         }
       }
       zero_acc();
@@ -1691,21 +1659,21 @@ uint32_t lds_bytes(const GemvArgs &a, bool aq4) {
   return (rows + 1) * a.k * 2 + (aq4 ? rows * (a.k / 128) * 4 : 0);
 }
 
-template <int MT, int WAVES>
+template <int MT, int WAVES, int EPI>
 hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
   if (vec && lds_allowed() && lds_bytes(a, false) <= lds_cap(false)) {
     if (a.units % (WAVES * kFp8LdsBatch) == 0) {
-      return launch_lds(fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, true>,
+      return launch_lds(fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, true, EPI>,
                         grid, dim3(WAVES * kWave), lds_bytes(a, false), s, a);
     }
-    return launch_lds(fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, false>,
+    return launch_lds(fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, false, EPI>,
                       grid, dim3(WAVES * kWave), lds_bytes(a, false), s, a);
   } else if (vec) {
-    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, true>), grid,
+    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, true, EPI>), grid,
                        dim3(WAVES * kWave), 0, s, a);
   } else {
-    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, false>), grid,
+    hipLaunchKernelGGL((fp8_gemv_kernel<MT, WAVES, false, EPI>), grid,
                        dim3(WAVES * kWave), 0, s, a);
   }
   return hipGetLastError();
@@ -1873,18 +1841,18 @@ hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
   return launch_lds(kernel, grid, dim3(waves * kWave), lds, s, a);
 }
 
-template <int MT, int NR, int P>
+template <int MT, int NR, int P, int EPI>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
       aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch,
-                         kAq4Ms.depth, NR, P>,
+                         kAq4Ms.depth, NR, P, EPI>,
       a, kAq4Ms.waves, ms_lds_bytes(a, true), s, kAq4Ms.waves / kAq4Ms.ks);
 }
 
-template <int MT>
+template <int MT, int EPI>
 hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
-      fp8_gemv_ms_kernel<MT, kFp8Ms.waves, kFp8Ms.batch, kFp8Ms.depth>, a,
+      fp8_gemv_ms_kernel<MT, kFp8Ms.waves, kFp8Ms.batch, kFp8Ms.depth, EPI>, a,
       kFp8Ms.waves, ms_lds_bytes(a, false), s);
 }
 
@@ -1929,8 +1897,8 @@ hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
   return hipGetLastError();
 }
 
-#define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P>
-template <int MT, int P>
+#define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P, EPI>
+template <int MT, int P, int EPI>
 hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
@@ -1939,7 +1907,7 @@ hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
-template <int MT, int P>
+template <int MT, int P, int EPI>
 hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
@@ -1967,21 +1935,21 @@ int rs_pack(const GemvArgs &a, const RsCfg *c, bool aq4) {
 }
 #undef ULLM_RS_KERNEL
 
-template <int MT, int WAVES>
+template <int MT, int WAVES, int EPI>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
   if (vec && lds_allowed() && lds_bytes(a, true) <= lds_cap(true)) {
     if (a.units % (WAVES * kAq4LdsBatch) == 0) {
-      return launch_lds(aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, true>,
+      return launch_lds(aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, true, EPI>,
                         grid, dim3(WAVES * kWave), lds_bytes(a, true), s, a);
     }
-    return launch_lds(aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, false>,
+    return launch_lds(aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, false, EPI>,
                       grid, dim3(WAVES * kWave), lds_bytes(a, true), s, a);
   } else if (vec) {
-    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, true>), grid,
+    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, true, EPI>), grid,
                        dim3(WAVES * kWave), 0, s, a);
   } else {
-    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, false>), grid,
+    hipLaunchKernelGGL((aq4_gemv_kernel<MT, WAVES, false, EPI>), grid,
                        dim3(WAVES * kWave), 0, s, a);
   }
   return hipGetLastError();
@@ -1999,73 +1967,92 @@ bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
 
 }  // namespace
 
-hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
+template <int EPI>
+hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 64);
   const bool two = a.m > 16;
   // FP8 keeps the LDS-staged kernel where the activation block fits (M=8
   // 4096->28672: 21.0 against 25.3 us register-staged); AQ4, whose per-byte
   // work is heavier, gains from the register-staged kernel there too.
   if (use_ms(a, vec, two ? 2 : 1, false)) {
-    return two ? launch_fp8_ms<2>(a, s) : launch_fp8_ms<1>(a, s);
+    return two ? launch_fp8_ms<2, EPI>(a, s) : launch_fp8_ms<1, EPI>(a, s);
   }
   // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
   if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec) : nullptr) {
     if (two) {
-      return launch_fp8_rs<2, 1>(a, rs, s);
+      return launch_fp8_rs<2, 1, EPI>(a, rs, s);
     }
-    return rs_pack(a, rs, false) == 2 ? launch_fp8_rs<1, 2>(a, rs, s)
-                                  : launch_fp8_rs<1, 1>(a, rs, s);
+    return rs_pack(a, rs, false) == 2 ? launch_fp8_rs<1, 2, EPI>(a, rs, s)
+                                  : launch_fp8_rs<1, 1, EPI>(a, rs, s);
   }
   const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
-    case 4: return launch_fp8_t<1, 2>(a, vec, s);
-    case 5: return launch_fp8_t<2, 2>(a, vec, s);
-    case 8: return launch_fp8_t<1, 4>(a, vec, s);
-    case 9: return launch_fp8_t<2, 4>(a, vec, s);
-    case 16: return launch_fp8_t<1, 8>(a, vec, s);
-    case 17: return launch_fp8_t<2, 8>(a, vec, s);
-    case 32: return launch_fp8_t<1, 16>(a, vec, s);
-    default: return launch_fp8_t<2, 16>(a, vec, s);
+    case 4: return launch_fp8_t<1, 2, EPI>(a, vec, s);
+    case 5: return launch_fp8_t<2, 2, EPI>(a, vec, s);
+    case 8: return launch_fp8_t<1, 4, EPI>(a, vec, s);
+    case 9: return launch_fp8_t<2, 4, EPI>(a, vec, s);
+    case 16: return launch_fp8_t<1, 8, EPI>(a, vec, s);
+    case 17: return launch_fp8_t<2, 8, EPI>(a, vec, s);
+    case 32: return launch_fp8_t<1, 16, EPI>(a, vec, s);
+    default: return launch_fp8_t<2, 16, EPI>(a, vec, s);
   }
 }
 
-hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
+template <int EPI>
+hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
   if (const RsCfg *rs = plan_rs(a, vec)) {
     if (two) {
-      return launch_aq4_rs<2, 1>(a, rs, s);
+      return launch_aq4_rs<2, 1, EPI>(a, rs, s);
     }
     switch (rs_pack(a, rs, true)) {
-      case 4: return launch_aq4_rs<1, 4>(a, rs, s);
-      case 2: return launch_aq4_rs<1, 2>(a, rs, s);
-      default: return launch_aq4_rs<1, 1>(a, rs, s);
+      case 4: return launch_aq4_rs<1, 4, EPI>(a, rs, s);
+      case 2: return launch_aq4_rs<1, 2, EPI>(a, rs, s);
+      default: return launch_aq4_rs<1, 1, EPI>(a, rs, s);
     }
   }
   if (use_ms(a, vec, two ? 2 : 1, true)) {
     if (two) {
-      return launch_aq4_ms<2, 4, 1>(a, s);
+      return launch_aq4_ms<2, 4, 1, EPI>(a, s);
     }
     // Rows packed four classes deep up to M = 4 (ULLM_GEMV_PACK < 4 turns
     // this off).
     static const int cap = env_int("ULLM_GEMV_PACK", 4);
     if (a.m > 4 || cap < 4) {
-      return launch_aq4_ms<1, 4, 1>(a, s);
+      return launch_aq4_ms<1, 4, 1, EPI>(a, s);
     }
-    return a.m == 1 ? launch_aq4_ms<1, 1, 4>(a, s)
-                    : a.m == 2 ? launch_aq4_ms<1, 2, 4>(a, s)
-                               : launch_aq4_ms<1, 4, 4>(a, s);
+    return a.m == 1 ? launch_aq4_ms<1, 1, 4, EPI>(a, s)
+                    : a.m == 2 ? launch_aq4_ms<1, 2, 4, EPI>(a, s)
+                               : launch_aq4_ms<1, 4, 4, EPI>(a, s);
   }
   const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
   switch (waves * 2 + (two ? 1 : 0)) {
-    case 4: return launch_aq4_t<1, 2>(a, vec, s);
-    case 5: return launch_aq4_t<2, 2>(a, vec, s);
-    case 8: return launch_aq4_t<1, 4>(a, vec, s);
-    case 9: return launch_aq4_t<2, 4>(a, vec, s);
-    case 16: return launch_aq4_t<1, 8>(a, vec, s);
-    case 17: return launch_aq4_t<2, 8>(a, vec, s);
-    case 32: return launch_aq4_t<1, 16>(a, vec, s);
-    default: return launch_aq4_t<2, 16>(a, vec, s);
+    case 4: return launch_aq4_t<1, 2, EPI>(a, vec, s);
+    case 5: return launch_aq4_t<2, 2, EPI>(a, vec, s);
+    case 8: return launch_aq4_t<1, 4, EPI>(a, vec, s);
+    case 9: return launch_aq4_t<2, 4, EPI>(a, vec, s);
+    case 16: return launch_aq4_t<1, 8, EPI>(a, vec, s);
+    case 17: return launch_aq4_t<2, 8, EPI>(a, vec, s);
+    case 32: return launch_aq4_t<1, 16, EPI>(a, vec, s);
+    default: return launch_aq4_t<2, 16, EPI>(a, vec, s);
+  }
+}
+
+// The epilogue kind is a template parameter of every kernel: dispatch once.
+hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s) {
+  switch (a.epi.kind) {
+    case kEpiSiluMul: return fp8_gemv_e<kEpiSiluMul>(a, s);
+    case kEpiResidual: return fp8_gemv_e<kEpiResidual>(a, s);
+    default: return fp8_gemv_e<kEpiNone>(a, s);
+  }
+}
+
+hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
+  switch (a.epi.kind) {
+    case kEpiSiluMul: return aq4_gemv_e<kEpiSiluMul>(a, s);
+    case kEpiResidual: return aq4_gemv_e<kEpiResidual>(a, s);
+    default: return aq4_gemv_e<kEpiNone>(a, s);
   }
 }
 

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "device_common.hpp"
 #include "layout.hpp"
 
 namespace ullm {
@@ -50,6 +51,7 @@ struct GemvArgs {
   float alpha;
   bool y_f32;
   uint32_t spw;        // stripes per workgroup (multi-stripe kernels; set by the launcher)
+  Epilogue epi;        // output epilogue (n_out = output columns)
 };
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s);
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s);

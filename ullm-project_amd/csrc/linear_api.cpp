@@ -26,7 +26,7 @@ namespace ullm {
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            const ullm_linear_weight_t *w, uint32_t m,
                            void *y, uint64_t ldy, bool y_f32, float alpha,
-                           hipStream_t s);
+                           const Epilogue &epi, hipStream_t s);
 }  // namespace ullm
 
 namespace {
@@ -148,9 +148,13 @@ ullm_status_t validate_weight_desc(const ullm_linear_weight_desc_t *d,
   if (st != ULLM_STATUS_OK) {
     return st;
   }
-  if (!ullm::all_zero(d->reserved)) {
+  if (!ullm::all_zero(d->reserved) || d->reserved0 != 0) {
     return write_error(sink, ULLM_STATUS_RESERVED_NONZERO,
                        "weight descriptor reserved fields must be zero");
+  }
+  if (d->layout != ULLM_LINEAR_LAYOUT_PLAIN &&
+      d->layout != ULLM_LINEAR_LAYOUT_GATED_PAIRS) {
+    return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT, "unknown weight layout");
   }
   if (d->encoding != ULLM_LINEAR_ENCODING_FP8_E4M3_ROW &&
       d->encoding != ULLM_LINEAR_ENCODING_AQ4_G128) {
@@ -172,6 +176,10 @@ ullm_status_t validate_weight_desc(const ullm_linear_weight_desc_t *d,
   if (d->n > kMaxDim || d->k > kMaxDim) {
     return write_error(sink, ULLM_STATUS_UNSUPPORTED,
                        "weight dimension exceeds 2^31 - 1");
+  }
+  if (d->layout == ULLM_LINEAR_LAYOUT_GATED_PAIRS && d->n % 2 != 0) {
+    return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                       "a gated-pair weight needs an even N (gate rows, then up rows)");
   }
   if (d->encoding == ULLM_LINEAR_ENCODING_AQ4_G128 && d->k % 128 != 0) {
     return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
@@ -224,14 +232,15 @@ ullm_status_t create_weight(const ullm_linear_weight_desc_t *d,
   w->device = d->device;
   w->n = d->n;
   w->k = d->k;
+  w->gate = d->layout == ULLM_LINEAR_LAYOUT_GATED_PAIRS ? d->n / 2 : 0;
   const hipStream_t stream = static_cast<hipStream_t>(d->stream);
   const bool fp8 = d->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
   if (fp8) {
-    w->fp8 = ullm::make_fp8_layout(d->n, d->k);
+    w->fp8 = ullm::make_fp8_layout(d->n, d->k, w->gate);
     w->tile_bytes = w->fp8.bytes();
     w->aux_bytes = w->fp8.n16 * sizeof(float);
   } else {
-    w->aq4 = ullm::make_aq4_layout(d->n, d->k);
+    w->aq4 = ullm::make_aq4_layout(d->n, d->k, w->gate);
     w->tile_bytes = w->aq4.words() * sizeof(uint32_t);
     w->aux_bytes = w->aq4.sz_words() * sizeof(uint32_t);
   }
@@ -347,9 +356,46 @@ ullm_status_t validate_forward(const ullm_linear_forward_desc_t *d,
     return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
                        "x_row_stride is smaller than K");
   }
-  if (d->y_row_stride != 0 && d->y_row_stride < w->n) {
+  if (d->epilogue != ULLM_LINEAR_EPILOGUE_NONE &&
+      d->epilogue != ULLM_LINEAR_EPILOGUE_SILU_MUL &&
+      d->epilogue != ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD) {
+    return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT, "unknown epilogue");
+  }
+  const bool gated = w->gate != 0;
+  if (gated != (d->epilogue == ULLM_LINEAR_EPILOGUE_SILU_MUL)) {
     return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
-                       "y_row_stride is smaller than N");
+                       gated ? "a gated-pair weight needs the SILU_MUL epilogue"
+                             : "SILU_MUL needs a gated-pair weight");
+  }
+  const uint64_t n_out = gated ? w->gate : w->n;
+  if (d->y_row_stride != 0 && d->y_row_stride < n_out) {
+    return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                       "y_row_stride is smaller than the output width");
+  }
+  if (d->epilogue == ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD) {
+    if (d->residual_dtype != ULLM_LINEAR_DTYPE_BF16 &&
+        d->residual_dtype != ULLM_LINEAR_DTYPE_F32) {
+      return write_error(sink, ULLM_STATUS_UNSUPPORTED,
+                         "residual dtype must be bf16 or f32");
+    }
+    if (d->residual_row_stride != 0 && d->residual_row_stride < w->n) {
+      return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "residual_row_stride is smaller than N");
+    }
+    if (d->m != 0 && d->residual == nullptr) {
+      return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "residual pointer is null");
+    }
+    const uint64_t ldr = d->residual_row_stride ? d->residual_row_stride : w->n;
+    const uint64_t ldy = d->y_row_stride ? d->y_row_stride : w->n;
+    if (d->residual == d->y && (d->residual_dtype != d->y_dtype || ldr != ldy)) {
+      return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "an in-place residual must match y's dtype and row stride");
+    }
+  } else if (d->residual != nullptr || d->residual_dtype != 0 ||
+             d->residual_row_stride != 0) {
+    return write_error(sink, ULLM_STATUS_INVALID_ARGUMENT,
+                       "residual fields are set without the RESIDUAL_ADD epilogue");
   }
   if (d->m > 65535ULL * 32ULL) {
     return write_error(sink, ULLM_STATUS_UNSUPPORTED,
@@ -438,7 +484,7 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_weight_query(
     if (st != ULLM_STATUS_OK) {
       return st;
     }
-    if (!ullm::all_zero(info->reserved)) {
+    if (!ullm::all_zero(info->reserved) || info->reserved0 != 0) {
       return write_error(error_sink, ULLM_STATUS_RESERVED_NONZERO,
                          "weight info reserved fields must be zero");
     }
@@ -447,6 +493,8 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_weight_query(
     info->n = weight->n;
     info->k = weight->k;
     info->device_bytes = weight->tile_bytes + weight->aux_bytes;
+    info->layout = weight->gate != 0 ? ULLM_LINEAR_LAYOUT_GATED_PAIRS
+                                     : ULLM_LINEAR_LAYOUT_PLAIN;
     return ULLM_STATUS_OK;
   });
 }
@@ -590,9 +638,19 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
     HIP_TRY(error_sink, "hipSetDevice", scope.error());
     const hipStream_t s = static_cast<hipStream_t>(desc->stream);
     const uint64_t ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
-    const uint64_t ldy = desc->y_row_stride ? desc->y_row_stride : w->n;
+    const uint64_t n_out = w->gate != 0 ? w->gate : w->n;
+    const uint64_t ldy = desc->y_row_stride ? desc->y_row_stride : n_out;
     const bool y_f32 = desc->y_dtype == ULLM_LINEAR_DTYPE_F32;
     const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
+    ullm::Epilogue epi{};
+    epi.kind = desc->epilogue == ULLM_LINEAR_EPILOGUE_SILU_MUL ? ullm::kEpiSiluMul
+               : desc->epilogue == ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD
+                   ? ullm::kEpiResidual
+                   : ullm::kEpiNone;
+    epi.n_out = static_cast<uint32_t>(n_out);
+    epi.res = desc->residual;
+    epi.ldr = desc->residual_row_stride ? desc->residual_row_stride : w->n;
+    epi.res_f32 = desc->residual_dtype == ULLM_LINEAR_DTYPE_F32;
 
     if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 &&
         desc->activation_mode == ULLM_LINEAR_ACT_EXACT) {
@@ -608,6 +666,7 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
       a.k = static_cast<uint32_t>(w->k);
       a.alpha = desc->alpha;
       a.y_f32 = y_f32;
+      a.epi = epi;
       if (fp8w) {
         a.n16 = static_cast<uint32_t>(w->fp8.n16);
         a.units = static_cast<uint32_t>(w->fp8.blocks_per_stripe());
@@ -664,7 +723,7 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
     }
     HIP_TRY(error_sink, "fp8 gemm kernel",
             ullm::launch_fp8_gemm(xq, xs, ldxq, w, static_cast<uint32_t>(desc->m),
-                                  desc->y, ldy, y_f32, desc->alpha, s));
+                                  desc->y, ldy, y_f32, desc->alpha, epi, s));
     return ULLM_STATUS_OK;
   });
 }

@@ -9,6 +9,7 @@ struct ullm_linear_weight_t {
   uint32_t encoding = 0;
   int device = 0;
   uint64_t n = 0, k = 0;
+  uint64_t gate = 0;  // F of a gated-pair weight (N = 2F), 0 for a plain one
   ullm::Fp8Layout fp8{};
   ullm::Aq4Layout aq4{};
   void *tiles = nullptr;  // FP8: u8 wave tiles; AQ4: u32 wave tiles

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kBlock) void fp8_quantize_kernel(
   amax = block_max(amax, red);
   const float s = amax / 448.0f;
   if (threadIdx.x == 0) {
-    scales[row] = s;
+    scales[L.phys(row)] = s;
   }
   for (uint64_t c = threadIdx.x; c < L.k; c += kBlock) {
     const uint32_t q = s == 0.0f ? 0u : f32_to_e4m3(src[c] / s);
@@ -62,7 +62,7 @@ __global__ __launch_bounds__(kBlock) void fp8_pack_kernel(
     const uint64_t row = i / L.k, col = i % L.k;
     tiles[L.offset(row, col)] = q[i];
     if (col == 0) {
-      scales[row] = s_in[row];
+      scales[L.phys(row)] = s_in[row];
     }
   }
 }
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kBlock) void fp8_export_kernel(
     const uint64_t row = i / L.k, col = i % L.k;
     q[i] = tiles[L.offset(row, col)];
     if (col == 0) {
-      s_out[row] = scales[row];
+      s_out[row] = scales[L.phys(row)];
     }
   }
 }
@@ -88,19 +88,23 @@ __global__ __launch_bounds__(kBlock) void fp8_dequant_kernel(
   for (uint64_t i = blockIdx.x * uint64_t(kBlock) + threadIdx.x; i < total;
        i += uint64_t(gridDim.x) * kBlock) {
     const uint64_t row = i / L.k, col = i % L.k;
-    out[i] = e4m3_to_f32(tiles[L.offset(row, col)]) * scales[row];
+    out[i] = e4m3_to_f32(tiles[L.offset(row, col)]) * scales[L.phys(row)];
   }
 }
 
 // ---------------------------------------------------------------- AQ4 g128
+// Dword and scale|zero word of canonical row `row` (placed at its physical
+// row).
 __device__ __forceinline__ uint64_t aq4_word(const Aq4Layout &L, uint64_t row,
                                              uint64_t g, uint32_t q4,
                                              uint32_t j) {
-  return (((row / 16) * L.groups + g) * 64 + (row % 16) + 16 * q4) * 4 + j;
+  const uint64_t p = L.phys(row);
+  return (((p / 16) * L.groups + g) * 64 + (p % 16) + 16 * q4) * 4 + j;
 }
 __device__ __forceinline__ uint64_t aq4_sz(const Aq4Layout &L, uint64_t row,
                                            uint64_t g) {
-  return ((row / 16) * L.groups + g) * 16 + row % 16;
+  const uint64_t p = L.phys(row);
+  return ((p / 16) * L.groups + g) * 16 + p % 16;
 }
 
 // One wavefront per (row, group of 128).

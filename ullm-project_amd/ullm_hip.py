@@ -67,6 +67,11 @@ DTYPE_F32 = 2
 DTYPE_F8E4M3FN = 3
 ACT_EXACT = 0
 ACT_FP8_PER_TOKEN = 1
+LAYOUT_PLAIN = 0
+LAYOUT_GATED_PAIRS = 1
+EPILOGUE_NONE = 0
+EPILOGUE_SILU_MUL = 1
+EPILOGUE_RESIDUAL_ADD = 2
 BACKEND_HIP = 1
 
 # ------------------------------------------------------------------- structs
@@ -104,13 +109,14 @@ class WeightDesc(ctypes.Structure):
                 ("encoding", _u32), ("source", _u32), ("n", _u64), ("k", _u64),
                 ("memory", _u32), ("device", _i32), ("values", _vp),
                 ("scales", _vp), ("zeros", _vp), ("stream", _vp),
-                ("reserved", _u64 * 4)]
+                ("layout", _u32), ("reserved0", _u32), ("reserved", _u64 * 3)]
 
 
 class WeightInfo(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("abi_version", _u32),
                 ("encoding", _u32), ("device", _i32), ("n", _u64), ("k", _u64),
-                ("device_bytes", _u64), ("reserved", _u64 * 4)]
+                ("device_bytes", _u64), ("layout", _u32), ("reserved0", _u32),
+                ("reserved", _u64 * 3)]
 
 
 class ForwardDesc(ctypes.Structure):
@@ -119,7 +125,9 @@ class ForwardDesc(ctypes.Structure):
                 ("x_scales", _vp), ("y", _vp), ("y_row_stride", _u64),
                 ("x_dtype", _u32), ("y_dtype", _u32), ("activation_mode", _u32),
                 ("alpha", ctypes.c_float), ("stream", _vp), ("workspace", _vp),
-                ("workspace_size", _u64), ("reserved", _u64 * 4)]
+                ("workspace_size", _u64), ("epilogue", _u32),
+                ("residual_dtype", _u32), ("residual", _vp),
+                ("residual_row_stride", _u64), ("reserved", _u64 * 1)]
 
 
 class ActQuantDesc(ctypes.Structure):
@@ -255,30 +263,42 @@ def _stream(stream):
 
 
 class LinearWeight:
-    """A device-resident quantized weight W[N][K] (opaque native handle)."""
+    """A device-resident quantized weight W[N][K] (opaque native handle).
 
-    def __init__(self, handle: int, encoding: int, n: int, k: int, device: int):
+    ``gated=True`` (ULLM_LINEAR_LAYOUT_GATED_PAIRS) marks a fused gate/up
+    projection whose N = 2F rows are the F gate rows followed by the F up
+    rows; its forward applies SiLU(gate) * up and returns F columns."""
+
+    def __init__(self, handle: int, encoding: int, n: int, k: int, device: int,
+                 gated: bool = False):
         self.handle = handle
         self.encoding = encoding
         self.n = n
         self.k = k
         self.device = device
+        self.gated = gated
+
+    @property
+    def n_out(self) -> int:
+        """Output columns of a forward: F = N / 2 for a gated pair, else N."""
+        return self.n // 2 if self.gated else self.n
 
     # -- construction -----------------------------------------------------
     @classmethod
     def _create(cls, encoding, source, n, k, memory, device, values, scales=None,
-                zeros=None, stream=None):
+                zeros=None, stream=None, gated=False):
         s = _Sink()
         d = new(WeightDesc, encoding=encoding, source=source, n=n, k=k,
                 memory=memory, device=device, values=values, scales=scales,
-                zeros=zeros, stream=stream)
+                zeros=zeros, stream=stream,
+                layout=LAYOUT_GATED_PAIRS if gated else LAYOUT_PLAIN)
         h = _vp()
         _check(lib().ullm_linear_weight_create(ctypes.byref(d), ctypes.byref(h),
                                                s.ref), s)
-        return cls(h.value, encoding, n, k, device)
+        return cls(h.value, encoding, n, k, device, gated)
 
     @classmethod
-    def quantize(cls, w, encoding: int, stream=None):
+    def quantize(cls, w, encoding: int, stream=None, gated=False):
         """Quantize an f32 weight tensor [N][K] (CUDA or CPU) on the GPU."""
         import torch
         assert w.dtype == torch.float32 and w.dim() == 2
@@ -286,28 +306,31 @@ class LinearWeight:
         n, k = w.shape
         if w.is_cuda:
             return cls._create(encoding, SOURCE_F32, n, k, MEMORY_DEVICE,
-                               w.device.index, _ptr(w), stream=_stream(stream))
+                               w.device.index, _ptr(w), stream=_stream(stream),
+                               gated=gated)
         return cls._create(encoding, SOURCE_F32, n, k, MEMORY_HOST, 0, _ptr(w),
-                           stream=None)
+                           stream=None, gated=gated)
 
     @classmethod
-    def from_fp8(cls, q, s, device=0, stream=None):
+    def from_fp8(cls, q, s, device=0, stream=None, gated=False):
         """Upload canonical E4M3 codes q uint8 [N][K] and f32 scales [N]."""
         n, k = q.shape
         mem = MEMORY_DEVICE if getattr(q, "is_cuda", False) else MEMORY_HOST
         return cls._create(ENCODING_FP8_E4M3_ROW, SOURCE_ENCODED, n, k, mem,
                            device, _addr(q), _addr(s), None,
-                           _stream(stream) if mem == MEMORY_DEVICE else None)
+                           _stream(stream) if mem == MEMORY_DEVICE else None,
+                           gated=gated)
 
     @classmethod
-    def from_aq4(cls, packed, scales, zeros, device=0, stream=None):
+    def from_aq4(cls, packed, scales, zeros, device=0, stream=None, gated=False):
         """Upload canonical AQ4: u32 [N][K/8], f16 bits [N][K/128] x 2."""
         n = packed.shape[0]
         k = packed.shape[1] * 8
         mem = MEMORY_DEVICE if getattr(packed, "is_cuda", False) else MEMORY_HOST
         return cls._create(ENCODING_AQ4_G128, SOURCE_ENCODED, n, k, mem, device,
                            _addr(packed), _addr(scales), _addr(zeros),
-                           _stream(stream) if mem == MEMORY_DEVICE else None)
+                           _stream(stream) if mem == MEMORY_DEVICE else None,
+                           gated=gated)
 
     # -- lifetime ----------------------------------------------------------
     def destroy(self):
@@ -366,7 +389,8 @@ class LinearWeight:
         d = new(ForwardDesc, weight=self.handle, m=m, x=_ptr(probe),
                 x_row_stride=0, x_scales=_ptr(probe), y=_ptr(probe),
                 y_row_stride=0, x_dtype=x_dtype, y_dtype=DTYPE_BF16,
-                activation_mode=mode, alpha=1.0)
+                activation_mode=mode, alpha=1.0,
+                epilogue=EPILOGUE_SILU_MUL if self.gated else EPILOGUE_NONE)
         out = _u64(0)
         s = _Sink()
         _check(lib().ullm_linear_workspace_size(ctypes.byref(d), ctypes.byref(out),
@@ -374,16 +398,26 @@ class LinearWeight:
         return int(out.value)
 
     def forward(self, x, y=None, *, x_scales=None, out_dtype=None, alpha=1.0,
-                mode=ACT_EXACT, stream=None, workspace=None):
+                mode=ACT_EXACT, stream=None, workspace=None, residual=None):
         """y = alpha * x @ W^T for x bf16 [M][>=K] (row stride honoured) or
-        pre-quantized e4m3 (uint8) with x_scales."""
+        pre-quantized e4m3 (uint8) with x_scales.  A gated-pair weight returns
+        silu(gate) * up (F columns); ``residual`` (bf16 or f32 [M][>=N], may
+        be ``y`` itself) is added to the product (ULLM_LINEAR_EPILOGUE_*)."""
         import torch
         m = x.shape[0]
         if y is None:
             dt = out_dtype or torch.bfloat16
-            y = torch.empty((m, self.n), dtype=dt, device=x.device)
+            y = torch.empty((m, self.n_out), dtype=dt, device=x.device)
         x_dtype = DTYPE_F8E4M3FN if x.dtype in (torch.uint8, torch.float8_e4m3fn) \
             else DTYPE_BF16
+        epi = EPILOGUE_SILU_MUL if self.gated else EPILOGUE_NONE
+        res = {}
+        if residual is not None:
+            epi = EPILOGUE_RESIDUAL_ADD
+            res = dict(residual=_ptr(residual),
+                       residual_row_stride=residual.stride(0),
+                       residual_dtype=DTYPE_F32 if residual.dtype == torch.float32
+                       else DTYPE_BF16)
         d = new(ForwardDesc, weight=self.handle, m=m, x=_ptr(x),
                 x_row_stride=x.stride(0) if x.dim() == 2 else 0,
                 x_scales=_ptr(x_scales), y=_ptr(y), y_row_stride=y.stride(0),
@@ -391,7 +425,8 @@ class LinearWeight:
                 y_dtype=DTYPE_F32 if y.dtype == torch.float32 else DTYPE_BF16,
                 activation_mode=mode, alpha=alpha, stream=_stream(stream),
                 workspace=_ptr(workspace),
-                workspace_size=0 if workspace is None else workspace.numel() * workspace.element_size())
+                workspace_size=0 if workspace is None else workspace.numel() * workspace.element_size(),
+                epilogue=epi, **res)
         s = _Sink()
         _check(lib().ullm_linear_forward(ctypes.byref(d), s.ref), s)
         return y
