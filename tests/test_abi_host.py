@@ -66,6 +66,14 @@ int main(void) {
   F(ullm_linear_forward_desc_t, residual_row_stride) F(ullm_linear_forward_desc_t, reserved)
   S(ullm_linear_act_quant_desc_t) F(ullm_linear_act_quant_desc_t, xq) F(ullm_linear_act_quant_desc_t, reserved)
   S(ullm_linear_weight_export_desc_t) F(ullm_linear_weight_export_desc_t, values) F(ullm_linear_weight_export_desc_t, reserved)
+  S(ullm_safetensors_open_desc_t) F(ullm_safetensors_open_desc_t, expected_sha256) F(ullm_safetensors_open_desc_t, reserved)
+  S(ullm_safetensors_tensor_info_t) F(ullm_safetensors_tensor_info_t, shape) F(ullm_safetensors_tensor_info_t, offset)
+  F(ullm_safetensors_tensor_info_t, reserved)
+  S(ullm_linear_weight_load_desc_t) F(ullm_linear_weight_load_desc_t, values) F(ullm_linear_weight_load_desc_t, value_parts)
+  F(ullm_linear_weight_load_desc_t, device) F(ullm_linear_weight_load_desc_t, scales) F(ullm_linear_weight_load_desc_t, stream)
+  F(ullm_linear_weight_load_desc_t, reserved)
+  S(ullm_linear_weights_save_desc_t) F(ullm_linear_weights_save_desc_t, weights) F(ullm_linear_weights_save_desc_t, metadata_count)
+  F(ullm_linear_weights_save_desc_t, reserved)
   return 0;
 }
 """
@@ -90,6 +98,10 @@ def test_headers_compile_and_layout_matches_ctypes(uh, tmp_path):
         "ullm_linear_forward_desc_t": uh.ForwardDesc,
         "ullm_linear_act_quant_desc_t": uh.ActQuantDesc,
         "ullm_linear_weight_export_desc_t": uh.ExportDesc,
+        "ullm_safetensors_open_desc_t": uh.StOpenDesc,
+        "ullm_safetensors_tensor_info_t": uh.StTensorInfo,
+        "ullm_linear_weight_load_desc_t": uh.WeightLoadDesc,
+        "ullm_linear_weights_save_desc_t": uh.WeightsSaveDesc,
     }
     for line in out.splitlines():
         key, value = line.rsplit(" ", 1)

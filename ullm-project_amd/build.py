@@ -20,8 +20,8 @@ BUILD = PKG / "_build"
 LIB = PKG / "lib" / "libullm_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["abi_v1.cpp", "linear_api.cpp", "weights.hip", "gemv.hip",
-           "gemm_fp8.hip"]
+SOURCES = ["abi_v1.cpp", "linear_api.cpp", "safetensors.cpp", "weights.hip",
+           "gemv.hip", "gemm_fp8.hip"]
 
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",

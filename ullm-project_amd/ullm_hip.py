@@ -142,6 +142,41 @@ class ExportDesc(ctypes.Structure):
                 ("zeros", _vp), ("stream", _vp), ("reserved", _u64 * 4)]
 
 
+class StOpenDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("path", ctypes.c_char_p),
+                ("expected_sha256", _vp), ("expected_size", _u64),
+                ("reserved", _u64 * 4)]
+
+
+class StTensorInfo(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("dtype", _u32),
+                ("rank", _u32), ("shape", _u64 * 8), ("offset", _u64),
+                ("bytes", _u64), ("reserved", _u64 * 4)]
+
+
+class WeightLoadDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("file", _vp),
+                ("encoding", _u32), ("layout", _u32),
+                ("values", ctypes.POINTER(ctypes.c_char_p)), ("value_parts", _u32),
+                ("device", _i32), ("scales", ctypes.c_char_p), ("zeros", ctypes.c_char_p),
+                ("stream", _vp), ("reserved", _u64 * 4)]
+
+
+class WeightsSaveDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("path", ctypes.c_char_p),
+                ("names", ctypes.POINTER(ctypes.c_char_p)),
+                ("weights", ctypes.POINTER(_vp)), ("count", _u64),
+                ("metadata_keys", ctypes.POINTER(ctypes.c_char_p)),
+                ("metadata_values", ctypes.POINTER(ctypes.c_char_p)),
+                ("metadata_count", _u64), ("reserved", _u64 * 4)]
+
+
+# safetensors dtype strings by ULLM_ST_DTYPE_* value
+ST_DTYPES = {1: "BOOL", 2: "U8", 3: "I8", 4: "F8_E4M3", 5: "F8_E5M2", 6: "U16",
+             7: "I16", 8: "F16", 9: "BF16", 10: "U32", 11: "I32", 12: "F32",
+             13: "U64", 14: "I64", 15: "F64"}
+
+
 def new(struct_type, **fields):
     """A struct with its {struct_size, abi_version} header filled in."""
     s = struct_type()
@@ -173,6 +208,21 @@ _SIGNATURES = {
                                    ctypes.POINTER(ErrorSink)],
     "ullm_linear_quantize_activations": [ctypes.POINTER(ActQuantDesc),
                                          ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_open": [ctypes.POINTER(StOpenDesc), ctypes.POINTER(_vp),
+                              ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_close": [ctypes.POINTER(_vp), ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_tensor_count": [_vp, ctypes.POINTER(_u64), ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_tensor_name": [_vp, _u64, ctypes.c_char_p, _u64,
+                                     ctypes.POINTER(_u64), ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_tensor_info": [_vp, ctypes.c_char_p, ctypes.POINTER(StTensorInfo),
+                                     ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_metadata": [_vp, ctypes.c_char_p, ctypes.c_char_p, _u64,
+                                  ctypes.POINTER(_u64), ctypes.POINTER(ErrorSink)],
+    "ullm_safetensors_file_sha256": [_vp, ctypes.c_char_p, ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weight_load": [ctypes.POINTER(WeightLoadDesc), ctypes.POINTER(_vp),
+                                ctypes.POINTER(ErrorSink)],
+    "ullm_linear_weights_save": [ctypes.POINTER(WeightsSaveDesc), ctypes.c_char_p,
+                                 ctypes.POINTER(ErrorSink)],
 }
 
 _lib = None
@@ -438,6 +488,148 @@ def _addr(a):
     if hasattr(a, "data_ptr"):
         return int(a.data_ptr())
     return int(a.ctypes.data)
+
+
+# ------------------------------------------------------------ weight files
+
+def _cstrs(items):
+    arr = (ctypes.c_char_p * len(items))()
+    for i, v in enumerate(items):
+        arr[i] = v.encode() if isinstance(v, str) else v
+    return arr
+
+
+def _string_call(fn, *args):
+    """Call a string-returning entry point, growing the buffer on demand."""
+    cap = 256
+    while True:
+        buf = ctypes.create_string_buffer(cap)
+        n = _u64(0)
+        s = _Sink()
+        st = fn(*args, buf, cap, ctypes.byref(n), s.ref)
+        if st == Status.BUFFER_TOO_SMALL and n.value + 1 > cap:
+            cap = n.value + 1
+            continue
+        _check(st, s)
+        return buf.raw[:n.value].decode()
+
+
+class SafetensorsFile:
+    """An open, validated safetensors file (ullm_safetensors_open).
+
+    ``sha256`` (hex string or 32 bytes) and ``size`` make the open check the
+    file's content against a model lock's record before anything is read."""
+
+    def __init__(self, path, sha256=None, size=None):
+        digest = None
+        if sha256 is not None:
+            digest = bytes.fromhex(sha256) if isinstance(sha256, str) else bytes(sha256)
+            assert len(digest) == 32
+        self._digest = ctypes.create_string_buffer(digest, 32) if digest else None
+        d = new(StOpenDesc, path=str(path).encode(),
+                expected_sha256=ctypes.cast(self._digest, _vp) if digest else None,
+                expected_size=size or 0)
+        h = _vp()
+        s = _Sink()
+        _check(lib().ullm_safetensors_open(ctypes.byref(d), ctypes.byref(h), s.ref), s)
+        self.handle = h.value
+        self.path = str(path)
+
+    def close(self):
+        if self.handle:
+            h = _vp(self.handle)
+            self.handle = None
+            s = _Sink()
+            _check(lib().ullm_safetensors_close(ctypes.byref(h), s.ref), s)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def names(self):
+        n = _u64(0)
+        s = _Sink()
+        _check(lib().ullm_safetensors_tensor_count(self.handle, ctypes.byref(n), s.ref), s)
+        return [_string_call(lib().ullm_safetensors_tensor_name, self.handle, i)
+                for i in range(n.value)]
+
+    def info(self, name):
+        """(dtype string, shape tuple, byte offset in the file, byte count)."""
+        i = new(StTensorInfo)
+        s = _Sink()
+        _check(lib().ullm_safetensors_tensor_info(self.handle, name.encode(),
+                                                  ctypes.byref(i), s.ref), s)
+        return ST_DTYPES[i.dtype], tuple(i.shape[:i.rank]), i.offset, i.bytes
+
+    def metadata(self, key):
+        return _string_call(lib().ullm_safetensors_metadata, self.handle, key.encode())
+
+    def sha256(self) -> str:
+        out = ctypes.create_string_buffer(32)
+        s = _Sink()
+        _check(lib().ullm_safetensors_file_sha256(self.handle, out, s.ref), s)
+        return out.raw.hex()
+
+
+def load_weight(file, values, encoding, *, scales=None, zeros=None, gated=False,
+                device=0, stream=None):
+    """A LinearWeight from tensors of an open SafetensorsFile
+    (ullm_linear_weight_load).  ``values``: one tensor name, or a list of float
+    tensors stacked along N (e.g. [gate, up] for a gated pair)."""
+    parts = [values] if isinstance(values, str) else list(values)
+    arr = _cstrs(parts)
+    d = new(WeightLoadDesc, file=file.handle, encoding=encoding,
+            layout=LAYOUT_GATED_PAIRS if gated else LAYOUT_PLAIN,
+            values=arr, value_parts=len(parts), device=device,
+            scales=scales.encode() if scales else None,
+            zeros=zeros.encode() if zeros else None,
+            stream=_stream(stream) if stream is not None else None)
+    h = _vp()
+    s = _Sink()
+    _check(lib().ullm_linear_weight_load(ctypes.byref(d), ctypes.byref(h), s.ref), s)
+    w = LinearWeight(h.value, encoding, 0, 0, device, gated)
+    info = w.info()
+    w.n, w.k = int(info.n), int(info.k)
+    return w
+
+
+def load_saved_weight(file, name, device=0, stream=None):
+    """A weight written by save_weights, by its name (encoding and layout from
+    the file's metadata)."""
+    enc = file.metadata(f"{name}.encoding")
+    gated = file.metadata(f"{name}.layout") == "gated_pairs"
+    if enc == "fp8_e4m3_row":
+        return load_weight(file, f"{name}.weight", ENCODING_FP8_E4M3_ROW,
+                           scales=f"{name}.weight_scale", gated=gated, device=device,
+                           stream=stream)
+    if enc == "aq4_g128":
+        return load_weight(file, f"{name}.qweight", ENCODING_AQ4_G128,
+                           scales=f"{name}.scales", zeros=f"{name}.zeros", gated=gated,
+                           device=device, stream=stream)
+    raise ValueError(f"unknown encoding {enc!r} for {name}")
+
+
+def save_weights(path, weights, metadata=None) -> str:
+    """Write {name: LinearWeight} in canonical encodings (ullm_linear_weights_save);
+    returns the file's SHA-256 (hex)."""
+    names = list(weights)
+    harr = (_vp * len(names))(*[weights[n].handle for n in names])
+    meta = dict(metadata or {})
+    d = new(WeightsSaveDesc, path=str(path).encode(), names=_cstrs(names),
+            weights=harr, count=len(names), metadata_keys=_cstrs(list(meta)),
+            metadata_values=_cstrs(list(meta.values())), metadata_count=len(meta))
+    out = ctypes.create_string_buffer(32)
+    s = _Sink()
+    _check(lib().ullm_linear_weights_save(ctypes.byref(d), out, s.ref), s)
+    return out.raw.hex()
 
 
 def quantize_activations(x, stream=None):
