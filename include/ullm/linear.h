@@ -144,7 +144,10 @@ typedef struct ullm_linear_forward_desc_t {
   uint32_t activation_mode; /* ULLM_LINEAR_ACT_*, for BF16 x */
   float alpha;              /* output multiplier; 1.0f for a plain product */
   void *stream;
-  void *workspace; /* device scratch for ACT_FP8_PER_TOKEN; null = library-owned */
+  /* Device scratch (ullm_linear_workspace_size bytes) for ACT_FP8_PER_TOKEN
+   * and for split-K decode calls; null = library-owned.  For split-K calls
+   * it must be zero before its first use (each call leaves it so). */
+  void *workspace;
   uint64_t workspace_size;
   uint32_t epilogue;            /* ULLM_LINEAR_EPILOGUE_* (0 = none) */
   uint32_t residual_dtype;      /* RESIDUAL_ADD: BF16 or F32 */
@@ -216,8 +219,10 @@ ULLM_HIP_API ullm_status_t ullm_linear_weight_dequantize(
 ULLM_HIP_API ullm_status_t ullm_linear_forward(
     const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink);
 
-/* Bytes of workspace ullm_linear_forward needs for this descriptor (0 for the
- * exact path). */
+/* Bytes of workspace ullm_linear_forward needs for this descriptor: the
+ * per-token activation quantization of the prefill path, or the split-K
+ * scratch of a decode call that splits K (9 <= M <= 32, few output rows,
+ * long K); 0 when the call needs none. */
 ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
     const ullm_linear_forward_desc_t *desc, uint64_t *bytes,
     ullm_error_sink_t *error_sink);

@@ -1171,6 +1171,52 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
   }
 }
 
+// Split K.  With few stripes and a long K, the register-staged kernels split
+// each stripe group's K over a.ksplit workgroups (so that groups of S
+// stripes, which share their activation loads, still fill the chip).  Each
+// workgroup writes its fp32 partial sums to a.part; the last of the ksplit
+// workgroups to arrive at the group's counter adds them in fixed order
+// (deterministic) and stores the output.  No workgroup waits for another:
+// the counter only elects the finisher, which also resets it to zero for the
+// next call.  Partial slot of (k part, stripe T, row, column):
+// ((kp * stripes + T) * rows + row) * 16 + column, rows = MT * 16.
+//
+// The workgroups of a group may sit on different XCDs, whose L2 caches are
+// not coherent with each other.  Instead of device-scope fences (each one
+// writes back or invalidates a whole L2), the partial sums are stored and
+// loaded with the system-coherent cache policy (sc0 sc1), which goes to
+// memory, and the counter is a device-scope atomic issued after this
+// workgroup's stores have completed.
+constexpr int kSc = 1 | 16;  // sc0 | sc1
+
+// Element i of the partial sums through a buffer descriptor over a.part
+// (the scratch stays below 2 GiB).
+__device__ __forceinline__ void sk_put(__amdgpu_buffer_rsrc_t part, uint64_t i, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), part,
+                                        uint32_t(i * 4), 0, kSc);
+}
+__device__ __forceinline__ float sk_get(__amdgpu_buffer_rsrc_t part, uint64_t i) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(part, uint32_t(i * 4), 0, kSc));
+}
+
+__device__ __forceinline__ bool sk_arrive(uint32_t *cnt, uint32_t ks,
+                                          uint32_t *flag) {
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores completed
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev + 1 == ks;
+    if (last) {
+      __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *flag = last ? 1u : 0u;
+  }
+  lds_barrier();
+  return *flag != 0;
+}
+
 // Register-staged multi-stripe FP8 kernel, for activation blocks too large
 // for LDS (M > 16 at K = 4096, or long K).  Each wave reads its K share of
 // the activations straight from L2 into registers and reuses them across S
@@ -1183,24 +1229,30 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 // == 0.  P = 2 packs the two 32-k blocks of a unit into one activation load
 // for M <= 8, as described at the AQ4 register-staged kernel; the two block
 // products accumulate separately and each lane keeps its own class's.
-template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI>
+template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI, bool SK>
 __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
     GemvArgs a) {
   static_assert(P == 1 || (P == 2 && MT == 1), "row packing: one m-tile");
   constexpr int XR = 2 / P;            // activation registers per unit
   constexpr uint32_t RP = 16 / P;      // rows per class
   __shared__ float red[2][WAVES * S * MT * 4 * kWave];
+  __shared__ uint32_t sk_flag;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t units = a.units;
   const uint32_t stripes = a.n16 / 16;
   const uint32_t G = (stripes + S - 1) / S;  // stripe groups
-  const uint32_t G0 = blockIdx.x * a.spw;
+  // Split K: workgroup kp of a group's a.ksplit streams K part kp.
+  const uint32_t ks = SK ? a.ksplit : 1u;
+  const uint32_t kp = SK ? blockIdx.x % ks : 0u;
+  const uint32_t G0 = (SK ? blockIdx.x / ks : blockIdx.x) * a.spw;
+  const __amdgpu_buffer_rsrc_t pbuf = byte_buffer(a.part, 0x7ffffff0u);
   const uint32_t nG = min(a.spw, G - G0);
   const uint32_t T0 = G0 * S;
   const uint32_t nT = min(nG * S, stripes - T0);  // stripes of the run
-  const uint32_t ub = units * wave / WAVES;
-  const uint32_t ue = units * (wave + 1) / WAVES;
+  const uint32_t upk = units / ks;  // units of a K part
+  const uint32_t ub = kp * upk + upk * wave / WAVES;
+  const uint32_t ue = kp * upk + upk * (wave + 1) / WAVES;
   const uint32_t nbw = (ue - ub) / B;
   const uint32_t NB = nG * nbw;
   const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
@@ -1342,8 +1394,41 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
             }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
-          store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n,
+          if constexpr (SK) {
+            // A ragged last group's missing stripes have no slot (slot
+            // stripes would alias the next K part's stripe 0).
+            if (Tg + s < stripes) {
+              sk_put(pbuf,
+                     ((uint64_t(kp) * stripes + Tg + s) * (MT * 16) + mt * 16 + mrow) * 16 +
+                         ncol,
+                     v);
+            }
+          } else {
+            store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n,
                     a.alpha * (bt.rs[s] * v), m < a.m);
+          }
+        }
+      }
+      if constexpr (SK) {
+        if (sk_arrive(a.cnt + G0 + cgp, ks, &sk_flag)) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            if (Tg + s >= stripes) {
+              break;
+            }
+            for (uint32_t o = threadIdx.x; o < MT * RP * 16; o += WAVES * kWave) {
+              const uint32_t mt = o / (RP * 16), mrow = (o % (RP * 16)) / 16;
+              const uint32_t ncol = o % 16;
+              float v = 0.0f;
+              for (uint32_t k = 0; k < ks; ++k) {
+                v += sk_get(pbuf, ((uint64_t(k) * stripes + Tg + s) * (MT * 16) +
+                                     mt * 16 + mrow) * 16 + ncol);
+              }
+              const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
+              store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n,
+                    a.alpha * (bt.rs[s] * v), m < a.m);
+            }
+          }
         }
       }
       zero_acc();
@@ -1383,7 +1468,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 // class); the class rows of a stripe are summed in the final reduction.  The
 // ones-MFMA of register t gives every class the sum over its own blocks, so
 // a group needs 4 / P sum MFMAs instead of 4.
-template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI>
+template <int MT, int WAVES, int S, int B, int DEPTH, int P, int EPI, bool SK>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
     GemvArgs a) {
   static_assert(P == 1 || MT == 1, "row packing needs a single m-tile");
@@ -1391,17 +1476,23 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
   constexpr int XR = 4 / P;            // activation registers per group
   constexpr uint32_t RP = 16 / P;      // rows per class
   __shared__ float red[2][WAVES * S * MT * 4 * kWave];
+  __shared__ uint32_t sk_flag;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t groups = a.units;
   const uint32_t stripes = a.n16 / 16;
   const uint32_t G = (stripes + S - 1) / S;  // stripe groups
-  const uint32_t G0 = blockIdx.x * a.spw;
+  // Split K: workgroup kp of a group's a.ksplit streams K part kp.
+  const uint32_t ks = SK ? a.ksplit : 1u;
+  const uint32_t kp = SK ? blockIdx.x % ks : 0u;
+  const uint32_t G0 = (SK ? blockIdx.x / ks : blockIdx.x) * a.spw;
+  const __amdgpu_buffer_rsrc_t pbuf = byte_buffer(a.part, 0x7ffffff0u);
   const uint32_t nG = min(a.spw, G - G0);
   const uint32_t T0 = G0 * S;
   const uint32_t nT = min(nG * S, stripes - T0);
-  const uint32_t ub = groups * wave / WAVES;
-  const uint32_t ue = groups * (wave + 1) / WAVES;
+  const uint32_t upk = groups / ks;  // units of a K part
+  const uint32_t ub = kp * upk + upk * wave / WAVES;
+  const uint32_t ue = kp * upk + upk * (wave + 1) / WAVES;
   const uint32_t nbw = (ue - ub) / B;
   const uint32_t NB = nG * nbw;
   const __amdgpu_buffer_rsrc_t wbuf = byte_buffer(
@@ -1568,8 +1659,41 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
             }
           }
           const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
-          store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * v,
+          if constexpr (SK) {
+            // A ragged last group's missing stripes have no slot (slot
+            // stripes would alias the next K part's stripe 0).
+            if (Tg + s < stripes) {
+              sk_put(pbuf,
+                     ((uint64_t(kp) * stripes + Tg + s) * (MT * 16) + mt * 16 + mrow) * 16 +
+                         ncol,
+                     v);
+            }
+          } else {
+            store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * v,
                     m < a.m);
+          }
+        }
+      }
+      if constexpr (SK) {
+        if (sk_arrive(a.cnt + G0 + cgp, ks, &sk_flag)) {
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            if (Tg + s >= stripes) {
+              break;
+            }
+            for (uint32_t o = threadIdx.x; o < MT * RP * 16; o += WAVES * kWave) {
+              const uint32_t mt = o / (RP * 16), mrow = (o % (RP * 16)) / 16;
+              const uint32_t ncol = o % 16;
+              float v = 0.0f;
+              for (uint32_t k = 0; k < ks; ++k) {
+                v += sk_get(pbuf, ((uint64_t(k) * stripes + Tg + s) * (MT * 16) +
+                                     mt * 16 + mrow) * 16 + ncol);
+              }
+              const uint32_t m = m0 + mt * 16 + mrow, n = (Tg + s) * 16 + ncol;
+              store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, a.alpha * v,
+                    m < a.m);
+            }
+          }
         }
       }
       zero_acc();
@@ -1897,7 +2021,7 @@ hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
   return hipGetLastError();
 }
 
-#define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P, EPI>
+#define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P, EPI, false>
 template <int MT, int P, int EPI>
 hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
@@ -1914,6 +2038,61 @@ hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
   return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
+}
+
+// Split-K configuration: groups of 4 stripes (shared activation loads), 4
+// waves, K split over ksplit workgroups per group.
+#ifndef ULLM_RS_SPLIT
+#define ULLM_RS_SPLIT 4, 1, 2, 4
+#endif
+constexpr RsCfg kRsSplit{ULLM_RS_SPLIT};
+
+// K parts per stripe group for this launch (1 = no split): 9 <= M <= 32
+// (one activation block), few stripes (< 384) and K >= 12288, with enough
+// parts that groups x parts fill every CU, each part whole batches per wave.
+// Measured on MI355X (N = 4096, K = 14336): FP8 M=16 17.3 against 18.7 us,
+// M=32 23.7 against 29.9 us; AQ4 M=16 15.1 against 17.2 us, M=32 22.1
+// against 29.8 us.  The finisher's round trips through memory (stores,
+// counter, partial loads: ~5 us) cost more than the split saves at M <= 8
+// (AQ4 M=8 14.3 against 11.8 us) and at K <= 8192.
+// ULLM_GEMV_SPLIT=0 disables, =N forces N parts where they divide.
+uint32_t plan_split(const GemvArgs &a, bool vec, uint32_t unit_k) {
+  static const int forced = env_int("ULLM_GEMV_SPLIT", -1);
+  const uint32_t stripes = a.n16 / 16;
+  const uint32_t k = a.units * unit_k;
+  if (forced == 0 || !vec || a.m > 32 || stripes >= 384 ||
+      (forced < 0 && (k < 12288 || a.m <= 8)) ||
+      uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31) ||
+      (uint64_t(a.m - 1) * a.ldx + a.k) * 2 >= (uint64_t(1) << 31)) {
+    return 1;
+  }
+  const uint32_t G = (stripes + kRsSplit.s - 1) / kRsSplit.s;
+  uint32_t ks = forced > 1 ? uint32_t(forced) : (cu_count() + G - 1) / G;
+  ks = std::min(ks, 16u);
+  const uint32_t per = uint32_t(kRsSplit.waves * kRsSplit.batch);
+  while (ks > 1 && a.units % (ks * per) != 0) {
+    --ks;
+  }
+  return ks;
+}
+
+uint64_t split_cnt_bytes(const GemvArgs &a) {
+  const uint32_t G = (a.n16 / 16 + kRsSplit.s - 1) / kRsSplit.s;
+  return (uint64_t(G) * 4 + 255) / 256 * 256;
+}
+uint64_t split_bytes(const GemvArgs &a, uint32_t ks) {
+  const uint64_t rows = a.m > 16 ? 32 : 16;
+  return split_cnt_bytes(a) + uint64_t(ks) * a.n16 * rows * 4;
+}
+
+// One workgroup per (stripe group, K part).
+template <typename Kernel>
+hipError_t launch_split(Kernel kernel, GemvArgs a, uint32_t ks, hipStream_t s) {
+  const uint32_t groups = (a.n16 / 16 + kRsSplit.s - 1) / kRsSplit.s;
+  a.spw = 1;
+  a.ksplit = ks;
+  hipLaunchKernelGGL(kernel, dim3(groups * ks), dim3(kRsSplit.waves * kWave), 0, s, a);
+  return hipGetLastError();
 }
 
 // Row packing of the register-staged kernels: the largest P <= the cap
@@ -1977,6 +2156,13 @@ hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
   if (use_ms(a, vec, two ? 2 : 1, false)) {
     return two ? launch_fp8_ms<2, EPI>(a, s) : launch_fp8_ms<1, EPI>(a, s);
   }
+  const uint32_t ks = a.cnt != nullptr && a.m >= 8 ? plan_split(a, vec, 64) : 1;
+  if (ks > 1) {
+    return two ? launch_split(fp8_gemv_rs_kernel<2, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
+                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s)
+               : launch_split(fp8_gemv_rs_kernel<1, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
+                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s);
+  }
   // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
   if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec) : nullptr) {
     if (two) {
@@ -2002,6 +2188,13 @@ template <int EPI>
 hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
+  const uint32_t ks = a.cnt != nullptr && a.m >= 4 ? plan_split(a, vec, 128) : 1;
+  if (ks > 1) {
+    return two ? launch_split(aq4_gemv_rs_kernel<2, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
+                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s)
+               : launch_split(aq4_gemv_rs_kernel<1, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
+                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s);
+  }
   if (const RsCfg *rs = plan_rs(a, vec)) {
     if (two) {
       return launch_aq4_rs<2, 1, EPI>(a, rs, s);
@@ -2055,5 +2248,20 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
     default: return aq4_gemv_e<kEpiNone>(a, s);
   }
 }
+
+uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4) {
+  if (aq4 ? a.m < 4 : a.m < 8) {
+    return 0;
+  }
+  const bool vec = x_vec_ok(a, aq4 ? 128 : 64);
+  if (!aq4 && use_ms(a, vec, a.m > 16 ? 2 : 1, false)) {
+    return 0;
+  }
+  GemvArgs probe = a;
+  const uint32_t ks = plan_split(probe, vec, aq4 ? 128 : 64);
+  return ks > 1 ? split_bytes(a, ks) : 0;
+}
+
+uint64_t gemv_scratch_part_offset(const GemvArgs &a) { return split_cnt_bytes(a); }
 
 }  // namespace ullm

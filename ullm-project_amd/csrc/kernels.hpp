@@ -52,8 +52,18 @@ struct GemvArgs {
   bool y_f32;
   uint32_t spw;        // stripes per workgroup (multi-stripe kernels; set by the launcher)
   Epilogue epi;        // output epilogue (n_out = output columns)
+  // Split-K scratch (null = no split): counters, zero on entry and left zero,
+  // and fp32 partial sums; the launcher sets ksplit.
+  uint32_t *cnt;
+  float *part;
+  uint32_t ksplit;
 };
 hipError_t launch_fp8_gemv(const GemvArgs &a, hipStream_t s);
 hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s);
+// Bytes of split-K scratch the launch for these arguments would use (0: it
+// does not split).  The first bytes are counters that must be zero.
+uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4);
+// Offset of the partial sums inside that scratch.
+uint64_t gemv_scratch_part_offset(const GemvArgs &a);
 
 }  // namespace ullm

@@ -51,6 +51,9 @@ struct Workspace {
 };
 std::mutex g_ws_mutex;
 Workspace g_ws[64];
+// Library-owned per-device split-K scratch of the decode path: its counter
+// words are zero on allocation and every launch leaves them zero.
+Workspace g_split_ws[64];
 
 // Makes `device` current for the scope and restores the caller's device.
 class DeviceScope {
@@ -618,7 +621,24 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
     }
     const bool quantize = desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 &&
                           desc->activation_mode == ULLM_LINEAR_ACT_FP8_PER_TOKEN;
-    *bytes = quantize ? prefill_workspace_bytes(desc->m, desc->weight->k) : 0;
+    const ullm_linear_weight_t *w = desc->weight;
+    if (quantize) {
+      *bytes = prefill_workspace_bytes(desc->m, w->k);
+    } else if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 && desc->m != 0) {
+      // Decode: split-K scratch when the launch would split K.
+      const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
+      ullm::GemvArgs a{};
+      a.x = static_cast<const uint16_t *>(desc->x);
+      a.ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
+      a.m = static_cast<uint32_t>(desc->m);
+      a.n = static_cast<uint32_t>(w->n);
+      a.k = static_cast<uint32_t>(w->k);
+      a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
+      a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
+      *bytes = ullm::gemv_scratch_bytes(a, !fp8w);
+    } else {
+      *bytes = 0;
+    }
     return ULLM_STATUS_OK;
   });
 }
@@ -667,6 +687,39 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
       a.alpha = desc->alpha;
       a.y_f32 = y_f32;
       a.epi = epi;
+      a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
+      a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
+      const uint64_t need = ullm::gemv_scratch_bytes(a, !fp8w);
+      if (need != 0) {
+        void *ws = desc->workspace;
+        if (ws != nullptr) {
+          if (desc->workspace_size < need) {
+            return write_errorf(error_sink, ULLM_STATUS_BUFFER_TOO_SMALL,
+                                "workspace needs " + std::to_string(need) + " bytes");
+          }
+        } else {
+          if (w->device >= 64) {
+            return write_error(error_sink, ULLM_STATUS_UNSUPPORTED,
+                               "library workspace supports device ordinals < 64");
+          }
+          std::lock_guard<std::mutex> lock(g_ws_mutex);
+          Workspace &cache = g_split_ws[w->device];
+          if (cache.bytes < need) {
+            if (cache.ptr != nullptr) {
+              HIP_TRY(error_sink, "hipFree (workspace)", hipFree(cache.ptr));
+              cache.ptr = nullptr;
+              cache.bytes = 0;
+            }
+            HIP_TRY(error_sink, "hipMalloc (workspace)", hipMalloc(&cache.ptr, need));
+            cache.bytes = need;
+            HIP_TRY(error_sink, "hipMemset (workspace)", hipMemset(cache.ptr, 0, need));
+          }
+          ws = cache.ptr;
+        }
+        a.cnt = static_cast<uint32_t *>(ws);
+        a.part = reinterpret_cast<float *>(static_cast<char *>(ws) +
+                                           ullm::gemv_scratch_part_offset(a));
+      }
       if (fp8w) {
         a.n16 = static_cast<uint32_t>(w->fp8.n16);
         a.units = static_cast<uint32_t>(w->fp8.blocks_per_stripe());
