@@ -43,7 +43,8 @@ def _replays_match(fn, out, reps=4):
 
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 @pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (8, 28672, 4096), (8, 4096, 14336),
-                                   (3, 1000, 512), (17, 6200, 1024)])
+                                   (3, 1000, 512), (17, 6200, 1024),
+                                   (24, 2000, 14336)])   # split K: counters reset
 def test_decode_forward_under_graph(uh, gpu, enc, m, n, k):
     code = uh.ENCODING_FP8_E4M3_ROW if enc == "fp8" else uh.ENCODING_AQ4_G128
     lw = uh.LinearWeight.quantize(torch.from_numpy(weights(n, k, tag=m)).to(gpu), code)
