@@ -232,6 +232,35 @@ def test_activation_quant_bit_exact(uh, orc, gpu, m, k):
     assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
 
 
+def test_activation_quant_special_rows(uh, orc, gpu):
+    """Rows that pin the encode: exact E4M3 ties (row max 448 makes the scale
+    1.0, so the midpoints between codes are quotients as they stand), the
+    subnormal range, rows holding inf and NaN (inf max gives a NaN quotient
+    for inf and zero for finite values), NaN beside finite values, and the
+    bf16 extremes."""
+    k = 1024
+    codes = np.arange(0x7e, dtype=np.uint8)
+    vals = orc.e4m3_to_f32(codes).astype(np.float64)
+    mids = ((vals[:-1] + vals[1:]) / 2).astype(np.float32)
+    rows = []
+    r = np.zeros(k, np.float32)
+    r[0] = 448.0
+    r[1:1 + mids.size] = mids
+    r[1 + mids.size:1 + 2 * mids.size] = -mids
+    rows.append(r)
+    rows.append(np.linspace(-1e-3, 1e-3, k).astype(np.float32))
+    r = np.linspace(-3, 3, k).astype(np.float32); r[5] = np.inf; rows.append(r)
+    r = np.linspace(-3, 3, k).astype(np.float32); r[9] = np.nan; rows.append(r)
+    r = np.linspace(-3, 3, k).astype(np.float32); r[9] = np.nan; r[700] = -np.inf
+    rows.append(r)
+    r = np.full(k, 3.3895314e38, np.float32); r[::2] *= -1; r[3] = 1e-38; rows.append(r)
+    xb = orc.bf16_from_f32(np.stack(rows))
+    xq_ref, xs_ref = orc.act_quantize(xb)
+    xq, xs = uh.quantize_activations(to_torch_bf16(xb, gpu))
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    assert np.array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
+
+
 def test_activation_quant_strided_view(uh, orc, gpu):
     """A 16-byte aligned view with a padded row stride takes the vector path;
     an odd column offset the scalar one.  Both match the oracle."""

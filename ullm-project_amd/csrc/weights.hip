@@ -255,7 +255,9 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
   const uint64_t row = blockIdx.x;
   const uint16_t *src = x + row * ldx;
   u32x4 v[CH];
-  float amax = 0.0f;
+  // Row maximum of the bf16 magnitudes as integers: for non-NaN values the
+  // bit order is the value order, and any inf or NaN shows as >= 0x7f80.
+  u16x2 mx = {0, 0};
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
@@ -264,11 +266,28 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
     const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      amax = fmaxf(amax, fabsf(bf16_to_f32(uint16_t(w[e] & 0xffffu))));
-      amax = fmaxf(amax, fabsf(bf16_to_f32(uint16_t(w[e] >> 16))));
+      mx = __builtin_elementwise_max(
+          mx, __builtin_bit_cast(u16x2, w[e] & 0x7fff7fffu));
     }
   }
-  amax = block_max(amax, red);
+  const uint32_t mb = mx.x > mx.y ? mx.x : mx.y;
+  float amax = block_max(mb >= 0x7f80u ? __builtin_inff() : bits_f32(mb << 16), red);
+  const bool finite = amax != __builtin_inff();
+  if (!finite) {
+    // A row holding inf or NaN: max|x| over the non-NaN values, as fmaxf.
+    __syncthreads();
+    float am = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(w[e] & 0xffffu))));
+        am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(w[e] >> 16))));
+      }
+    }
+    amax = block_max(am, red);
+  }
   const float a = amax / 448.0f;
   if (threadIdx.x == 0) {
     xs[row] = a;
@@ -279,11 +298,30 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
     if (idx < k) {
       const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
       uint32_t out[2] = {0u, 0u};
+      if (finite && a != 0.0f) {
+        // Every quotient is finite with |x / a| <= 448 (one rounding of
+        // 448 at most above it), where the hardware E4M3 convert rounds to
+        // nearest even exactly like f32_to_e4m3; scale 1.0 leaves it plain.
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t h = uint16_t(e % 2 ? w[e / 2] >> 16 : w[e / 2] & 0xffffu);
-        const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(h) / a);
-        out[e / 4] |= q << (8 * (e % 4));
+        for (int d = 0; d < 2; ++d) {
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t ww = w[2 * d + e / 2];
+            f[e] = bf16_to_f32(uint16_t(e % 2 ? ww >> 16 : ww & 0xffffu)) / a;
+          }
+          s16x2 r = {0, 0};
+          r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, f[0], f[1], 1.0f, false);
+          r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, f[2], f[3], 1.0f, true);
+          out[d] = __builtin_bit_cast(uint32_t, r);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t h = uint16_t(e % 2 ? w[e / 2] >> 16 : w[e / 2] & 0xffffu);
+          const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(h) / a);
+          out[e / 4] |= q << (8 * (e % 4));
+        }
       }
       *reinterpret_cast<u32x2 *>(xq + row * k + idx) = u32x2{out[0], out[1]};
     }
