@@ -213,15 +213,22 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   // Workgroups are dispatched round-robin over the 8 XCDs; when the tile
   // count divides evenly, give each XCD a contiguous range of tiles so the
   // workgroups sharing one L2 also share operand tiles.
+  // A persistent grid walks tiles id = blockIdx.x + r * gridDim.x; with a
+  // grid that is a multiple of 8 every id of one workgroup stays on its XCD.
+  // Each tile's epilogue stores then drain under the next tile's first
+  // copies instead of at the end of a round of workgroups.
   const uint32_t total = mblocks * nblocks;
-  const uint32_t id = blockIdx.x;
+  const uint32_t stripes = (a.n + 15) / 16;
+  const uint32_t ksteps = a.k / C::BK;
+  const uint32_t wm = wave / C::WN, wn = wave % C::WN;
+  for (uint32_t id = blockIdx.x; id < total; id += gridDim.x) {
+  if (id != blockIdx.x) {
+    gemm_barrier();  // every wave is done reading the previous staged tile
+  }
   const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
   const uint32_t bm = tile % mblocks, bn = tile / mblocks;
   const uint32_t m0 = bm * C::BM;
   const uint32_t T0 = bn * (C::BN / 16);
-  const uint32_t stripes = (a.n + 15) / 16;
-  const uint32_t ksteps = a.k / C::BK;
-  const uint32_t wm = wave / C::WN, wn = wave % C::WN;
 
   // Per-lane copy sources, loop-invariant: a k-step only moves a uniform
   // base, so copies address memory as "scalar base + 32-bit lane offset".
@@ -425,7 +432,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         }
       }
     }
-    return;
+    continue;
   }
 #pragma unroll
   for (uint32_t i = 0; i < C::TM; ++i) {
@@ -440,6 +447,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
     }
   }
+  }  // tiles
 }
 
 using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
@@ -490,7 +498,15 @@ hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
   }
   const uint32_t tiles =
       ((a.m + C::BM - 1) / C::BM) * ((a.n + C::BN - 1) / C::BN);
-  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(tiles), dim3(C::WAVES * kWave),
+  // One workgroup per CU (the LDS holds one), looping over tiles.
+  // ULLM_GEMM_PERSIST=0 launches one workgroup per tile instead.
+  static const bool persist = [] {
+    const char *e = std::getenv("ULLM_GEMM_PERSIST");
+    return e == nullptr || e[0] != '0';
+  }();
+  static const uint32_t cus = gemm_cu_count() * (C::LDS <= 80 * 1024 ? 2 : 1);
+  const uint32_t grid = persist && tiles > cus ? cus : tiles;
+  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(grid), dim3(C::WAVES * kWave),
                      C::LDS, s, a);
   return hipGetLastError();
 }
