@@ -140,19 +140,25 @@ typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 #endif
 
 template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_,
-          uint32_t BSTAGES_ = 2>
+          uint32_t BSTAGES_ = 2, uint32_t ASTAGES_ = 2>
 struct GemmCfg {
   static constexpr uint32_t BM = BM_, BN = BN_, BK = 128, WM = WM_, WN = WN_;
   // A (activations, L2-resident) is double-buffered; B (weights, streamed
   // from HBM) may get a third buffer so its copies run two k-steps ahead.
   static constexpr uint32_t BSTAGES = BSTAGES_;
+  // A third A buffer lets the activation copies run two k-steps ahead
+  // (measured slower on MI355X at M=2048, N=28672, K=4096: 264-270 against
+  // 250-252 us, so the copies are not waiting on latency).
+  static constexpr uint32_t ASTAGES = ASTAGES_;
+  static_assert(ASTAGES >= 2 && ASTAGES <= 3 && BSTAGES >= 2 && BSTAGES <= 3,
+                "one or two k-steps of look-ahead");
   static constexpr uint32_t WAVES = WM * WN;
   static constexpr uint32_t TM = BM / WM / 16;  // 16-row m-tiles per wave
   static constexpr uint32_t TN = BN / WN / 16;  // 16-column n-tiles per wave
   static constexpr uint32_t A_TILES = BM / 16 * 2, B_TILES = BN / 16 * 2;
   static constexpr uint32_t A_BYTES = A_TILES * 1024;
   static constexpr uint32_t B_BYTES = B_TILES * 1024;
-  static constexpr uint32_t STAGE_BYTES = 2 * A_BYTES + BSTAGES * B_BYTES;
+  static constexpr uint32_t STAGE_BYTES = ASTAGES * A_BYTES + BSTAGES * B_BYTES;
   static constexpr uint32_t A_COPIES = A_TILES / WAVES;
   // B copies per wave; when the waves do not split B evenly, the last round
   // of copies is done by the first B_TILES % WAVES waves only.
@@ -202,6 +208,37 @@ __device__ __forceinline__ i32x8 lds_operand(const char *p) {
   return __builtin_bit_cast(i32x8, v);
 }
 
+// Four rows x one column per lane (an MFMA result) -> one row x four
+// columns: lanes 4g..4g+3 of a quad swap values so that lane 4g + q holds
+// row q of columns 4g..4g+3, as four bf16 in two dwords.  Two exchanges:
+// across lane bit 1 (row pairs), then across lane bit 0 (single rows).
+__device__ __forceinline__ u32x2 quad_transpose_bf16(f32x4 v, uint32_t lane) {
+  const uint32_t p01 = uint32_t(f32_to_bf16(v[0])) | (uint32_t(f32_to_bf16(v[1])) << 16);
+  const uint32_t p23 = uint32_t(f32_to_bf16(v[2])) | (uint32_t(f32_to_bf16(v[3])) << 16);
+  const bool b1 = lane & 2u, b0 = lane & 1u;
+  // After this, own = rows (2 b1, 2 b1 + 1) of my column, other = the same
+  // rows of column lane ^ 2.
+  const uint32_t send1 = b1 ? p01 : p23;
+  const uint32_t got1 = uint32_t(__shfl_xor(int(send1), 2, kWave));
+  const uint32_t own = b1 ? p23 : p01;
+  // Columns in quad order: c0 = lane & ~2 side, c2 = lane | 2 side.
+  const uint32_t lo_col = b1 ? got1 : own;   // column (lane & 1) of the pair (0/1)
+  const uint32_t hi_col = b1 ? own : got1;   // column (lane & 1) + 2
+  // Keep row 2 b1 + b0 of both columns, send the other row.
+  const uint32_t keep = b0 ? ((lo_col >> 16) | (hi_col & 0xffff0000u))
+                           : ((lo_col & 0xffffu) | (hi_col << 16));
+  const uint32_t send2 = b0 ? ((lo_col & 0xffffu) | (hi_col << 16))
+                            : ((lo_col >> 16) | (hi_col & 0xffff0000u));
+  const uint32_t got2 = uint32_t(__shfl_xor(int(send2), 1, kWave));
+  // keep = (col c, col c + 2) of my row, c = lane & 1; got2 = (col c ^ 1,
+  // col (c ^ 1) + 2).  Order as columns 0, 1, 2, 3.
+  const uint32_t c0 = b0 ? got2 : keep, c1 = b0 ? keep : got2;
+  u32x2 r;
+  r.x = (c0 & 0xffffu) | (c1 << 16);
+  r.y = (c0 >> 16) | (c1 & 0xffff0000u);
+  return r;
+}
+
 template <class C, uint32_t EPI>
 __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     GemmArgs a) {
@@ -210,55 +247,56 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t mblocks = (a.m + C::BM - 1) / C::BM;
   const uint32_t nblocks = (a.n + C::BN - 1) / C::BN;
-  // Workgroups are dispatched round-robin over the 8 XCDs; when the tile
-  // count divides evenly, give each XCD a contiguous range of tiles so the
-  // workgroups sharing one L2 also share operand tiles.
-  // A persistent grid walks tiles id = blockIdx.x + r * gridDim.x; with a
-  // grid that is a multiple of 8 every id of one workgroup stays on its XCD.
-  // Each tile's epilogue stores then drain under the next tile's first
-  // copies instead of at the end of a round of workgroups.
+  // A persistent grid walks tiles id = blockIdx.x + r * gridDim.x.  Tile ids
+  // are dispatched round-robin over the 8 XCDs; when the tile count divides
+  // evenly each XCD gets a contiguous range of tiles, so the workgroups
+  // sharing one L2 also share operand tiles, and with a grid that is a
+  // multiple of 8 every id of one workgroup stays on its XCD.
   const uint32_t total = mblocks * nblocks;
   const uint32_t stripes = (a.n + 15) / 16;
   const uint32_t ksteps = a.k / C::BK;
   const uint32_t wm = wave / C::WN, wn = wave % C::WN;
-  for (uint32_t id = blockIdx.x; id < total; id += gridDim.x) {
-  if (id != blockIdx.x) {
-    gemm_barrier();  // every wave is done reading the previous staged tile
-  }
-  const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
-  const uint32_t bm = tile % mblocks, bn = tile / mblocks;
-  const uint32_t m0 = bm * C::BM;
-  const uint32_t T0 = bn * (C::BN / 16);
+  // Plain bf16 output leaves the LDS alone: the next tile's first copies are
+  // issued before this tile's epilogue, so its stores and the refill of the
+  // pipeline overlap.  Fused epilogues stage whole rows through LDS.
+  constexpr bool direct_out = EPI == kEpiNone;
 
-  // Per-lane copy sources, loop-invariant: a k-step only moves a uniform
-  // base, so copies address memory as "scalar base + 32-bit lane offset".
-  // Tile (t, kb) of an operand sits at byte (t * 2 + kb) * 1024 of its half
-  // of the stage.  Rows past M and stripes past N repeat the last valid one;
-  // their results are never stored.
+  // Per-lane copy sources of the current tile, loop-invariant within it: a
+  // k-step only moves a uniform base, so copies address memory as "scalar
+  // base + 32-bit lane offset".  Tile (t, kb) of an operand sits at byte
+  // (t * 2 + kb) * 1024 of its half of the stage.  Rows past M and stripes
+  // past N repeat the last valid one; their results are never stored.
   uint32_t aoff[C::A_COPIES], boff[C::B_COPIES];
-  // A stage: 128 k-bytes of each of the block's rows, row-major (row r at
-  // r * 128), its eight 16-byte chunks XOR-swizzled with (r >> 1) & 7.  Each
-  // copy moves 8 whole rows: lane L fills slot L % 8 of row L / 8 from the
-  // row's chunk (L % 8) ^ swizzle, so every 8 lanes read one full 128-byte
-  // line of x, and the 16 rows an MFMA operand read touches (at one chunk)
-  // land in 16 different bank groups.
+  uint32_t m0 = 0, T0 = 0;
+  auto setup = [&](uint32_t id) {
+    const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
+    const uint32_t bm = tile % mblocks, bn = tile / mblocks;
+    m0 = bm * C::BM;
+    T0 = bn * (C::BN / 16);
+    // A stage: 128 k-bytes of each of the block's rows, row-major (row r at
+    // r * 128), its eight 16-byte chunks XOR-swizzled with (r >> 1) & 7.
+    // Each copy moves 8 whole rows: lane L fills slot L % 8 of row L / 8
+    // from the row's chunk (L % 8) ^ swizzle, so every 8 lanes read one full
+    // 128-byte line of x, and the 16 rows an MFMA operand read touches (at
+    // one chunk) land in 16 different bank groups.
 #pragma unroll
-  for (uint32_t i = 0; i < C::A_COPIES; ++i) {
-    const uint32_t r = (i * C::WAVES + wave) * 8 + lane / 8;
-    const uint32_t m = min(m0 + r, a.m - 1);
-    aoff[i] = m * uint32_t(a.ldxq) + (((lane % 8) ^ ((r >> 1) & 7)) * 16);
-  }
+    for (uint32_t i = 0; i < C::A_COPIES; ++i) {
+      const uint32_t r = (i * C::WAVES + wave) * 8 + lane / 8;
+      const uint32_t m = min(m0 + r, a.m - 1);
+      aoff[i] = m * uint32_t(a.ldxq) + (((lane % 8) ^ ((r >> 1) & 7)) * 16);
+    }
 #pragma unroll
-  for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-    const uint32_t c = min(i * C::WAVES + wave, C::B_TILES - 1);
-    const uint32_t t = c / 2, kb = c % 2;
-    const uint32_t T = min(T0 + t, stripes - 1);
-    boff[i] = (T * a.units + kb) * 1024 + lane * 16;
-  }
-  // LDS: A buffers [0, 2 * A_BYTES), then BSTAGES B buffers.
-  auto a_buf = [&](uint32_t ks) { return lds + (ks & 1) * C::A_BYTES; };
+    for (uint32_t i = 0; i < C::B_COPIES; ++i) {
+      const uint32_t c = min(i * C::WAVES + wave, C::B_TILES - 1);
+      const uint32_t t = c / 2, kb = c % 2;
+      const uint32_t T = min(T0 + t, stripes - 1);
+      boff[i] = (T * a.units + kb) * 1024 + lane * 16;
+    }
+  };
+  // LDS: ASTAGES A buffers, then BSTAGES B buffers.
+  auto a_buf = [&](uint32_t ks) { return lds + (ks % C::ASTAGES) * C::A_BYTES; };
   auto b_buf = [&](uint32_t ks) {
-    return lds + 2 * C::A_BYTES + (ks % C::BSTAGES) * C::B_BYTES;
+    return lds + C::ASTAGES * C::A_BYTES + (ks % C::BSTAGES) * C::B_BYTES;
   };
   auto copy_a = [&](uint32_t ks) {
     const uint8_t *abase = a.xq + uint64_t(ks) * C::BK;
@@ -279,6 +317,21 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     }
   };
   constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
+  constexpr uint32_t AAHEAD = C::ASTAGES - 1;  // k-steps A runs ahead
+  auto prologue = [&]() {
+#pragma unroll
+    for (uint32_t b = 0; b < AAHEAD; ++b) {
+      if (b < ksteps) {
+        copy_a(b);
+      }
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < BAHEAD; ++b) {
+      if (b < ksteps) {
+        copy_b(b);
+      }
+    }
+  };
   const uint32_t swz = (lane % 16) >> 1 & 7;
   const uint32_t a_lo = ((lane / 16) ^ swz) * 16;
   const uint32_t a_hi = ((4 + lane / 16) ^ swz) * 16;
@@ -290,6 +343,13 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     return __builtin_bit_cast(i32x8, v);
   };
 
+  uint32_t id = blockIdx.x;
+  if (id >= total) {
+    return;
+  }
+  setup(id);
+  prologue();
+  while (true) {
   f32x4 acc[C::TM][C::TN];
 #pragma unroll
   for (uint32_t i = 0; i < C::TM; ++i) {
@@ -298,27 +358,29 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-
-  copy_a(0);
-#pragma unroll
-  for (uint32_t b = 0; b < BAHEAD; ++b) {
-    if (b < ksteps) {
-      copy_b(b);
-    }
-  }
   __builtin_amdgcn_s_waitcnt(0);
   gemm_barrier();
 
   for (uint32_t ks = 0; ks < ksteps; ++ks) {
-    // Issue order A(ks + 1) then B(ks + BAHEAD): the in-order vector-memory
-    // counter then proves A(ks + 1) (and every older B) landed while the
-    // newest B copies stay in flight.
+    // Copies needed by step ks + 1 are issued before those two steps
+    // ahead: the in-order vector-memory counter then proves the former
+    // (and everything older) landed while the latter stay in flight.
+    const bool two_more = ks + 2 < ksteps;
     if (ks + 1 < ksteps) {
-      copy_a(ks + 1);
+      if (AAHEAD == 1) {
+        copy_a(ks + 1);
+      }
+      if (BAHEAD == 1) {
+        copy_b(ks + 1);
+      }
     }
-    const bool b_more = ks + BAHEAD < ksteps;
-    if (b_more) {
-      copy_b(ks + BAHEAD);
+    if (two_more) {
+      if (AAHEAD == 2) {
+        copy_a(ks + 2);
+      }
+      if (BAHEAD == 2) {
+        copy_b(ks + 2);
+      }
     }
     // Lane l's operand of m-tile i: row 16 i + l % 16 of the wave's rows,
     // k-bytes 16 (l / 16) .. (lo) and 64 + 16 (l / 16) .. (hi).
@@ -343,19 +405,39 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       af = an;
     }
-    if (b_more && BAHEAD > 1 && C::B_EVEN) {
-      wait_vm<C::B_COPIES>();
+    // Copies still allowed in flight: those issued for step ks + 2.  When
+    // the waves do not split B evenly, the last B round is issued by the
+    // first B_TILES % WAVES waves only.
+    constexpr uint32_t ahead2 = (AAHEAD == 2 ? C::A_COPIES : 0) +
+                                (BAHEAD == 2 ? C::B_COPIES : 0);
+    if constexpr (ahead2 > 0) {
+      if (!two_more) {
+        __builtin_amdgcn_s_waitcnt(0);
+      } else if (BAHEAD == 1 || C::B_EVEN || wave < C::B_TILES % C::WAVES) {
+        wait_vm<ahead2>();
+      } else {
+        wait_vm<ahead2 - 1>();
+      }
     } else {
       __builtin_amdgcn_s_waitcnt(0);
     }
     gemm_barrier();
   }
 
+  // The main loop ended on a barrier: every operand stage is free.
+  const uint32_t cm0 = m0, cT0 = T0;
+  const uint32_t next = id + gridDim.x;
+  const bool more = next < total;
+  if (direct_out && more) {
+    setup(next);
+    prologue();
+  }
+
   // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each
   // 16 x 16 tile.  Scales are gathered first (independent loads in flight
   // together).
   const uint32_t ncol = lane % 16, rq = 4 * (lane / 16);
-  const uint32_t mw = m0 + wm * C::TM * 16, nw = (T0 + wn * C::TN) * 16;
+  const uint32_t mw = cm0 + wm * C::TM * 16, nw = (cT0 + wn * C::TN) * 16;
   float sn[C::TN], sm[C::TM][4];
 #pragma unroll
   for (uint32_t j = 0; j < C::TN; ++j) {
@@ -368,10 +450,37 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
     }
   }
-  if (!a.y_f32 && a.y_vec) {
+  if (direct_out && !a.y_f32 && a.y_vec) {
+    // One 8-byte store per 16 x 16 tile and lane: after the quad transpose
+    // lane l holds row 4 (l / 16) + l % 4 of columns 4 ((l % 16) / 4) .. + 3.
+    const uint32_t row = rq + lane % 4, c4 = (ncol / 4) * 4;
+#pragma unroll
+    for (uint32_t i = 0; i < C::TM; ++i) {
+#pragma unroll
+      for (uint32_t j = 0; j < C::TN; ++j) {
+        f32x4 v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
+        }
+        const u32x2 t = quad_transpose_bf16(v, lane);
+        const uint32_t m = mw + i * 16 + row, n = nw + j * 16 + c4;
+        uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
+        if (m < a.m) {
+          if (n + 4 <= a.n) {
+            *reinterpret_cast<u32x2 *>(dst) = t;
+          } else {
+            const uint32_t w[2] = {t.x, t.y};
+            for (uint32_t e = 0; e < 4 && n + e < a.n; ++e) {
+              dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e % 2)));
+            }
+          }
+        }
+      }
+    }
+  } else if (!a.y_f32 && a.y_vec) {
     // bf16 out through LDS: scale, round and stage the tile, then write
-    // whole 16-byte row segments.  The main loop ended on a barrier, so the
-    // operand stages are free.  SiLU-gated output keeps 8 of every 16
+    // whole 16-byte row segments.  SiLU-gated output keeps 8 of every 16
     // columns (gate lanes, with the up value from lane ^ 8), so its staged
     // rows are half as wide.
     uint16_t *tile_out = reinterpret_cast<uint16_t *>(lds) +
@@ -432,20 +541,29 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         }
       }
     }
-    continue;
-  }
+  } else {
 #pragma unroll
-  for (uint32_t i = 0; i < C::TM; ++i) {
+    for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t m = mw + i * 16 + rq + r;
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = mw + i * 16 + rq + r;
 #pragma unroll
-      for (uint32_t j = 0; j < C::TN; ++j) {
-        const uint32_t n = nw + j * 16 + ncol;
-        const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
-        store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, v, m < a.m);
+        for (uint32_t j = 0; j < C::TN; ++j) {
+          const uint32_t n = nw + j * 16 + ncol;
+          const float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
+          store_out<EPI>(a.y, a.ldy, a.y_f32, a.epi, a.n, m, n, v, m < a.m);
+        }
       }
     }
+  }
+  if (!more) {
+    break;
+  }
+  id = next;
+  if (!direct_out) {
+    gemm_barrier();  // every wave is done reading its staged tile
+    setup(id);
+    prologue();
   }
   }  // tiles
 }
@@ -456,6 +574,7 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 // the CU count where 256-column tiles leave the last round half empty.
 using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_BSTAGES>;
 using GemmMid = GemmCfg<128, 128, 2, 2>;    // 2 workgroups per CU
+
 
 // Compute units of the current device.
 uint32_t gemm_cu_count() {
@@ -525,10 +644,11 @@ template <uint32_t EPI>
 hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
                   hipStream_t s) {
   if (vec && offsets_fit && a.k % 128 == 0 && a.m >= 128) {
-    return gemm_mid_forced() ? launch_gemm_lds<GemmMid, EPI>(a, s)
-                             : gemm_use_narrow(a.m, a.n)
-                                   ? launch_gemm_lds<GemmNarrow, EPI>(a, s)
-                                   : launch_gemm_lds<GemmLarge, EPI>(a, s);
+    if (gemm_mid_forced()) {
+      return launch_gemm_lds<GemmMid, EPI>(a, s);
+    }
+    return gemm_use_narrow(a.m, a.n) ? launch_gemm_lds<GemmNarrow, EPI>(a, s)
+                                     : launch_gemm_lds<GemmLarge, EPI>(a, s);
   }
   const dim3 grid((a.n + 63) / 64, (a.m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel<EPI>, grid, dim3(256), 0, s, a, vec);
