@@ -168,13 +168,10 @@ struct GemmCfg {
   // Epilogue staging of each wave's bf16 tile; rows padded by 16 bytes so
   // the row groups of one LDS store land in different banks.
   static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
-  static constexpr uint32_t OUT_BYTES = WAVES * TM * 16 * OUT_STRIDE * 2;
-  // Plain bf16 output is staged one 16-row m-tile per wave at a time, past
-  // the operand stages, so the stages stay free for the next tile's copies.
+  // bf16 output is staged one 16-row m-tile per wave at a time, past the
+  // operand stages, so the stages stay free for the next tile's copies.
   static constexpr uint32_t CHUNK_BYTES = 16 * OUT_STRIDE * 2;
-  static constexpr uint32_t PLAIN_BYTES = STAGE_BYTES + WAVES * CHUNK_BYTES;
-  static constexpr uint32_t LDS =
-      OUT_BYTES > PLAIN_BYTES ? OUT_BYTES : PLAIN_BYTES;
+  static constexpr uint32_t LDS = STAGE_BYTES + WAVES * CHUNK_BYTES;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
 
@@ -213,34 +210,34 @@ __device__ __forceinline__ i32x8 lds_operand(const char *p) {
 }
 
 // Four rows x one column per lane (an MFMA result) -> one row x four
-// columns: lanes 4g..4g+3 of a quad swap values so that lane 4g + q holds
-// row q of columns 4g..4g+3, as four bf16 in two dwords.  Two exchanges:
-// across lane bit 1 (row pairs), then across lane bit 0 (single rows).
-__device__ __forceinline__ u32x2 quad_transpose_bf16(f32x4 v, uint32_t lane) {
-  const uint32_t p01 = uint32_t(f32_to_bf16(v[0])) | (uint32_t(f32_to_bf16(v[1])) << 16);
-  const uint32_t p23 = uint32_t(f32_to_bf16(v[2])) | (uint32_t(f32_to_bf16(v[3])) << 16);
-  const bool b1 = lane & 2u, b0 = lane & 1u;
-  // After this, own = rows (2 b1, 2 b1 + 1) of my column, other = the same
-  // rows of column lane ^ 2.
-  const uint32_t send1 = b1 ? p01 : p23;
-  const uint32_t got1 = uint32_t(__shfl_xor(int(send1), 2, kWave));
-  const uint32_t own = b1 ? p23 : p01;
-  // Columns in quad order: c0 = lane & ~2 side, c2 = lane | 2 side.
-  const uint32_t lo_col = b1 ? got1 : own;   // column (lane & 1) of the pair (0/1)
-  const uint32_t hi_col = b1 ? own : got1;   // column (lane & 1) + 2
-  // Keep row 2 b1 + b0 of both columns, send the other row.
-  const uint32_t keep = b0 ? ((lo_col >> 16) | (hi_col & 0xffff0000u))
-                           : ((lo_col & 0xffffu) | (hi_col << 16));
-  const uint32_t send2 = b0 ? ((lo_col & 0xffffu) | (hi_col << 16))
-                            : ((lo_col >> 16) | (hi_col & 0xffff0000u));
-  const uint32_t got2 = uint32_t(__shfl_xor(int(send2), 1, kWave));
-  // keep = (col c, col c + 2) of my row, c = lane & 1; got2 = (col c ^ 1,
-  // col (c ^ 1) + 2).  Order as columns 0, 1, 2, 3.
-  const uint32_t c0 = b0 ? got2 : keep, c1 = b0 ? keep : got2;
-  u32x2 r;
-  r.x = (c0 & 0xffffu) | (c1 << 16);
-  r.y = (c0 >> 16) | (c1 & 0xffff0000u);
-  return r;
+// columns: within each lane quad, lane q ends with row q of the quad's four
+// columns, in column order.  Two exchanges: across lane bit 1 (row pairs),
+// then across lane bit 0 (single rows).
+__device__ __forceinline__ f32x4 quad_transpose_f32(f32x4 v, uint32_t lane) {
+  const uint32_t q = lane & 3u;
+  const bool b1 = q & 2u, b0 = q & 1u;
+  // Keep rows 2 b1, 2 b1 + 1 of my column c; the partner c ^ 2 sends its
+  // values of those rows.
+  const float k0 = b1 ? v[2] : v[0], k1 = b1 ? v[3] : v[1];
+  const float s0 = b1 ? v[0] : v[2], s1 = b1 ? v[1] : v[3];
+  const float g0 = __shfl_xor(s0, 2, kWave), g1 = __shfl_xor(s1, 2, kWave);
+  // Keep row 2 b1 + b0 of columns c and c ^ 2; the partner c ^ 1 sends the
+  // same row of columns c ^ 1 and c ^ 3.
+  const float own = b0 ? k1 : k0, par = b0 ? g1 : g0;
+  const float r1 = __shfl_xor(b0 ? k0 : k1, 1, kWave);
+  const float r3 = __shfl_xor(b0 ? g0 : g1, 1, kWave);
+  f32x4 out;
+#pragma unroll
+  for (uint32_t c = 0; c < 4; ++c) {
+    const uint32_t d = c ^ q;  // 0: own, 1: r1, 2: par, 3: r3
+    out[c] = d == 0 ? own : d == 1 ? r1 : d == 2 ? par : r3;
+  }
+  return out;
+}
+
+__device__ __forceinline__ u32x2 pack_bf16x4(f32x4 t) {
+  return u32x2{uint32_t(f32_to_bf16(t[0])) | (uint32_t(f32_to_bf16(t[1])) << 16),
+               uint32_t(f32_to_bf16(t[2])) | (uint32_t(f32_to_bf16(t[3])) << 16)};
 }
 
 template <class C, uint32_t EPI>
@@ -260,10 +257,6 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t stripes = (a.n + 15) / 16;
   const uint32_t ksteps = a.k / C::BK;
   const uint32_t wm = wave / C::WN, wn = wave % C::WN;
-  // Plain bf16 output leaves the LDS alone: the next tile's first copies are
-  // issued before this tile's epilogue, so its stores and the refill of the
-  // pipeline overlap.  Fused epilogues stage whole rows through LDS.
-  constexpr bool direct_out = EPI == kEpiNone;
 
   // Per-lane copy sources of the current tile, loop-invariant within it: a
   // k-step only moves a uniform base, so copies address memory as "scalar
@@ -432,7 +425,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t cm0 = m0, cT0 = T0;
   const uint32_t next = id + gridDim.x;
   const bool more = next < total;
-  if (direct_out && more) {
+  // The epilogue leaves the operand stages alone (its LDS chunk lies past
+  // them), so the next tile's first copies are issued before it.
+  if (more) {
     setup(next);
     prologue();
   }
@@ -454,21 +449,62 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       sm[i][r] = a.xs[min(mw + i * 16 + rq + r, a.m - 1)];
     }
   }
-  if (direct_out && !a.y_f32 && a.y_vec) {
+  if (!a.y_f32 && a.y_vec) {
     // Per m-tile: the quad transpose turns each 16 x 16 MFMA result into
-    // one row x four columns per lane, written to the wave's LDS chunk as 8
-    // bytes; the chunk's rows then leave as 16-byte segments, each row of
-    // the wave's tile one contiguous run, through non-temporal stores (the
-    // output is not read again by this launch, and whole segments need no
-    // write combining in L2).  Measured on MI355X at M=2048, N=28672,
-    // K=4096: 8-byte direct stores 267-272 us, staged with plain stores
-    // 273-280 us, staged with non-temporal stores 259-261 us.
+    // one row x four columns per lane (fp32), where the fused epilogue
+    // applies (a residual read as one 4-column vector, or silu(gate) * up
+    // with the up columns from lane ^ 8), and the rounded values go to the
+    // wave's LDS chunk as 8 bytes.  The chunk's rows then leave as 16-byte
+    // segments, each row of the wave's tile one contiguous run, through
+    // non-temporal stores (the output is not read again by this launch, and
+    // whole segments need no write combining in L2).  Measured on MI355X at
+    // M=2048, N=28672, K=4096: 8-byte direct stores 267-272 us, the whole
+    // tile staged with plain stores 273-280 us, staged with non-temporal
+    // stores 259-261 us, per m-tile chunk with non-temporal stores 245-247.
+    constexpr bool gated = EPI == kEpiSiluMul;
+    constexpr bool resid = EPI == kEpiResidual;
     uint16_t *chunk = reinterpret_cast<uint16_t *>(lds + C::STAGE_BYTES) +
                       wave * (C::CHUNK_BYTES / 2);
     const uint32_t row = rq + lane % 4, c4 = (ncol / 4) * 4;
-    constexpr uint32_t lpr = C::TN * 2, segs = 16 * lpr;
+    // Gated: lanes with c4 < 8 hold gate columns, those with c4 >= 8 the
+    // matching up columns; the output has 8 features per 16-column tile.
+    constexpr uint32_t tw = gated ? 8 : 16;  // output columns per tile
+    constexpr uint32_t lpr = C::TN * tw / 8, segs = 16 * lpr;
+    const uint32_t n0 = gated ? nw / 2 : nw;
+    const uint32_t nlim = gated ? a.epi.n_out : a.n;
+    // Residual read as 4-element vectors when rows and base allow it.
+    const bool res_vec =
+        resid && reinterpret_cast<uintptr_t>(a.epi.res) % 16 == 0 && a.epi.ldr % 4 == 0;
 #pragma unroll
     for (uint32_t i = 0; i < C::TM; ++i) {
+      const uint32_t m = mw + i * 16 + row;
+      f32x4 rv[C::TN];
+      if constexpr (resid) {
+        // All of the m-tile's residual loads are issued before any is used.
+#pragma unroll
+        for (uint32_t j = 0; j < C::TN; ++j) {
+          const uint32_t n = nw + j * 16 + c4;
+          rv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (m < a.m) {
+            const uint64_t ri = uint64_t(m) * a.epi.ldr + n;
+            const float *rf = static_cast<const float *>(a.epi.res) + ri;
+            const uint16_t *rh = static_cast<const uint16_t *>(a.epi.res) + ri;
+            if (res_vec && n + 4 <= a.n) {
+              if (a.epi.res_f32) {
+                rv[j] = *reinterpret_cast<const f32x4 *>(rf);
+              } else {
+                const u32x2 h = *reinterpret_cast<const u32x2 *>(rh);
+                rv[j] = f32x4{bits_f32(h.x << 16), bits_f32(h.x & 0xffff0000u),
+                              bits_f32(h.y << 16), bits_f32(h.y & 0xffff0000u)};
+              }
+            } else {
+              for (uint32_t e = 0; e < 4 && n + e < a.n; ++e) {
+                rv[j][e] = a.epi.res_f32 ? rf[e] : bf16_to_f32(rh[e]);
+              }
+            }
+          }
+        }
+      }
 #pragma unroll
       for (uint32_t j = 0; j < C::TN; ++j) {
         f32x4 v;
@@ -476,8 +512,28 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         for (int r = 0; r < 4; ++r) {
           v[r] = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
         }
-        *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 16 + c4) =
-            quad_transpose_bf16(v, lane);
+        f32x4 t = quad_transpose_f32(v, lane);
+        if constexpr (resid) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            t[e] += rv[j][e];
+          }
+        }
+        if constexpr (gated) {
+          f32x4 up;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            up[e] = __shfl_xor(t[e], 8, kWave);
+            t[e] = silu_f32(t[e]) * up[e];
+          }
+          if (c4 < 8) {
+            *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 8 + c4) =
+                pack_bf16x4(t);
+          }
+        } else {
+          *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 16 + c4) =
+              pack_bf16x4(t);
+        }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's chunk is written
 #pragma unroll
@@ -489,14 +545,14 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         const uint32_t rr = seg / lpr, c8 = (seg % lpr) * 8;
         const u32x4 w = *reinterpret_cast<const u32x4 *>(
             chunk + rr * C::OUT_STRIDE + c8);
-        const uint32_t m = mw + i * 16 + rr, n = nw + c8;
-        uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
-        if (m < a.m) {
-          if (n + 8 <= a.n) {
+        const uint32_t mo = mw + i * 16 + rr, n = n0 + c8;
+        uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(mo) * a.ldy + n;
+        if (mo < a.m) {
+          if (n + 8 <= nlim) {
             __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(dst));
           } else {
             const uint32_t e4[4] = {w.x, w.y, w.z, w.w};
-            for (uint32_t e = 0; e < 8 && n + e < a.n; ++e) {
+            for (uint32_t e = 0; e < 8 && n + e < nlim; ++e) {
               dst[e] = static_cast<uint16_t>(e4[e / 2] >> (16 * (e % 2)));
             }
           }
@@ -504,69 +560,6 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       // The next m-tile's chunk writes follow these reads in the wave's
       // in-order LDS queue.
-    }
-  } else if (!a.y_f32 && a.y_vec) {
-    // bf16 out through LDS: scale, round and stage the tile, then write
-    // whole 16-byte row segments.  SiLU-gated output keeps 8 of every 16
-    // columns (gate lanes, with the up value from lane ^ 8), so its staged
-    // rows are half as wide.
-    uint16_t *tile_out = reinterpret_cast<uint16_t *>(lds) +
-                         wave * C::TM * 16 * C::OUT_STRIDE;
-    constexpr bool gated = EPI == kEpiSiluMul;
-    constexpr bool resid = EPI == kEpiResidual;
-#pragma unroll
-    for (uint32_t i = 0; i < C::TM; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (uint32_t j = 0; j < C::TN; ++j) {
-          float v = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
-          uint16_t *dst = tile_out + (i * 16 + rq + r) * C::OUT_STRIDE;
-          if constexpr (gated) {
-            const float up = __shfl_xor(v, 8, kWave);
-            if (ncol < 8) {
-              dst[j * 8 + ncol] = f32_to_bf16(silu_f32(v) * up);
-            }
-          } else {
-            const uint32_t m = mw + i * 16 + rq + r, n = nw + j * 16 + ncol;
-            if (resid && m < a.m && n < a.n) {
-              const uint64_t ri = uint64_t(m) * a.epi.ldr + n;
-              v += a.epi.res_f32
-                       ? static_cast<const float *>(a.epi.res)[ri]
-                       : bf16_to_f32(static_cast<const uint16_t *>(a.epi.res)[ri]);
-            }
-            dst[j * 16 + ncol] = f32_to_bf16(v);
-          }
-        }
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's LDS writes are done
-    // 16-byte segments: TN * 2 per row of the wave's tile (TN gated), spread
-    // over the lanes row-major.
-    constexpr uint32_t lpr = gated ? C::TN : C::TN * 2, segs = C::TM * 16 * lpr;
-    const uint32_t n0 = gated ? nw / 2 : nw;
-    const uint32_t nlim = gated ? a.epi.n_out : a.n;
-#pragma unroll
-    for (uint32_t it = 0; it < (segs + kWave - 1) / kWave; ++it) {
-      const uint32_t seg = it * kWave + lane;
-      if (segs % kWave != 0 && seg >= segs) {
-        break;
-      }
-      const uint32_t row = seg / lpr, c8 = (seg % lpr) * 8;
-      const uint32_t m = mw + row, n = n0 + c8;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(
-          tile_out + row * C::OUT_STRIDE + c8);
-      uint16_t *dst = static_cast<uint16_t *>(a.y) + uint64_t(m) * a.ldy + n;
-      if (m < a.m) {
-        if (n + 8 <= nlim) {
-          *reinterpret_cast<u32x4 *>(dst) = v;
-        } else {
-          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-          for (uint32_t e = 0; e < 8 && n + e < nlim; ++e) {
-            dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e % 2)));
-          }
-        }
-      }
     }
   } else {
 #pragma unroll
@@ -587,11 +580,6 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     break;
   }
   id = next;
-  if (!direct_out) {
-    gemm_barrier();  // every wave is done reading its staged tile
-    setup(id);
-    prologue();
-  }
   }  // tiles
 }
 
