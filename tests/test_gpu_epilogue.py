@@ -144,6 +144,31 @@ def test_residual_add_prefill_gemm(uh, orc, gpu):
     assert_close(y32.cpu().numpy(), ref, what="gemm residual f32")
 
 
+@pytest.mark.parametrize("m,n,k,rdtype,pad", [(300, 1000, 512, "f32", 0),
+                                              (130, 37, 256, "bf16", 3),
+                                              (257, 448, 384, "bf16", 0),
+                                              (256, 300, 256, "f32", 1)])
+def test_residual_add_prefill_gemm_bf16_out(uh, orc, gpu, m, n, k, rdtype, pad):
+    """bf16 output through the staged GEMM epilogue: residual as 4-column
+    vectors (aligned rows) or element by element (odd row strides), ragged
+    M and N, f32 and bf16 residuals."""
+    q, s = orc.fp8_quantize_rows(weights(n, k, tag=n + k))
+    xb = activations_bf16(orc, m, k, tag=m + 910)
+    rb = activations_bf16(orc, m, n, tag=m + 920)
+    xq, xs = orc.act_quantize(xb)
+    ref = orc.fp8_gemm(xq, xs, q, s)[0] + orc.bf16_to_f32(rb)
+    lw = uh.LinearWeight.from_fp8(q, s)
+    x = to_torch_bf16(xb, gpu)
+    wide = torch.zeros((m, n + pad), dtype=torch.float32 if rdtype == "f32" else torch.bfloat16,
+                       device=gpu)
+    res = wide[:, :n]
+    res.copy_(to_torch_bf16(rb, gpu).to(wide.dtype))
+    y = lw.forward(x, mode=uh.ACT_FP8_PER_TOKEN, residual=res)
+    torch.cuda.synchronize()
+    assert_close(bf16_tensor_to_f32(y), ref, bf16_out=True,
+                 what=f"gemm residual {rdtype} pad {pad} {m}x{n}x{k}")
+
+
 def test_epilogue_validation(uh, orc, gpu):
     import ctypes
     q, s = orc.fp8_quantize_rows(weights(32, 64))
