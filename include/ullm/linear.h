@@ -146,7 +146,12 @@ typedef struct ullm_linear_forward_desc_t {
   void *stream;
   /* Device scratch (ullm_linear_workspace_size bytes) for ACT_FP8_PER_TOKEN
    * and for split-K decode calls; null = library-owned.  For split-K calls
-   * it must be zero before its first use (each call leaves it so). */
+   * it must be zero before its first use (each call leaves it so).  The
+   * library-owned buffers are one per device and stream (calls on one stream
+   * share them in stream order) and are allocated, or grown, by the first
+   * call that needs them: make that call outside stream capture.  A grown
+   * buffer's predecessor stays allocated, so graphs captured earlier remain
+   * valid. */
   void *workspace;
   uint64_t workspace_size;
   uint32_t epilogue;            /* ULLM_LINEAR_EPILOGUE_* (0 = none) */

@@ -85,3 +85,57 @@ def test_small_stack_step_under_graph(uh, gpu):
     _replays_match(lambda: st.step(), st.logits)
     assert torch.isfinite(st.logits.float()).all()
     st.destroy()
+
+
+def test_library_workspace_outgrown_after_capture(uh, gpu):
+    """A graph captured with the library-owned prefill workspace replays
+    correctly after a larger call on the same stream has grown that
+    workspace (the outgrown buffer stays allocated)."""
+    lw = uh.LinearWeight.quantize(torch.from_numpy(weights(512, 1024, tag=21)).to(gpu),
+                                  uh.ENCODING_FP8_E4M3_ROW)
+    xs = torch.randn(256, 1024, device=gpu).bfloat16()
+    ys = torch.empty(256, 512, device=gpu, dtype=torch.bfloat16)
+    xb = torch.randn(2048, 1024, device=gpu).bfloat16()
+    yb = torch.empty(2048, 512, device=gpu, dtype=torch.bfloat16)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lw.forward(xs, ys, mode=uh.ACT_FP8_PER_TOKEN)   # allocates for M = 256
+    s.synchronize()
+    ref = ys.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        lw.forward(xs, ys, mode=uh.ACT_FP8_PER_TOKEN)
+    with torch.cuda.stream(s):
+        lw.forward(xb, yb, mode=uh.ACT_FP8_PER_TOKEN)   # grows the buffer
+    s.synchronize()
+    for i in range(3):
+        ys.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ys, ref), f"replay {i} after the workspace grew"
+
+
+def test_library_workspace_per_stream(uh, gpu):
+    """Prefill calls on two streams at once use separate library-owned
+    workspaces: each matches its result computed alone."""
+    lw = uh.LinearWeight.quantize(torch.from_numpy(weights(2048, 2048, tag=22)).to(gpu),
+                                  uh.ENCODING_FP8_E4M3_ROW)
+    xa = torch.randn(1024, 2048, device=gpu).bfloat16()
+    xb = torch.randn(1024, 2048, device=gpu).bfloat16()
+    ra = lw.forward(xa, mode=uh.ACT_FP8_PER_TOKEN)
+    rb = lw.forward(xb, mode=uh.ACT_FP8_PER_TOKEN)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    ya = torch.empty_like(ra)
+    yb = torch.empty_like(rb)
+    for _ in range(2):                       # first round allocates
+        sa.wait_stream(torch.cuda.current_stream())
+        sb.wait_stream(torch.cuda.current_stream())
+        for _ in range(4):
+            lw.forward(xa, ya, mode=uh.ACT_FP8_PER_TOKEN, stream=sa)
+            lw.forward(xb, yb, mode=uh.ACT_FP8_PER_TOKEN, stream=sb)
+        torch.cuda.synchronize()
+        assert torch.equal(ya, ra)
+        assert torch.equal(yb, rb)

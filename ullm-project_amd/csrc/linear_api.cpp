@@ -13,7 +13,9 @@
 #include <cmath>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <unordered_set>
+#include <vector>
 
 #include "abi_common.hpp"
 #include "kernels.hpp"
@@ -44,16 +46,35 @@ bool registered(const ullm_linear_weight_t *w) {
   return g_registry.count(w) != 0;
 }
 
-// Library-owned per-device workspace for the prefill path (grown on demand).
+// Library-owned workspaces, one per (device, stream, kind) and grown on
+// demand: the prefill path's quantized activations, and the decode path's
+// split-K scratch (its counter words are zero on allocation and every launch
+// leaves them zero).  Calls on one stream are ordered, so they may share a
+// buffer; calls on different streams get different buffers.  A buffer that
+// is outgrown is retired, not freed: a HIP graph captured earlier may still
+// hold its address, and stays valid.
 struct Workspace {
   void *ptr = nullptr;
   uint64_t bytes = 0;
 };
+struct WorkspaceKey {
+  int device;
+  const void *stream;
+  bool split;
+  bool operator==(const WorkspaceKey &o) const {
+    return device == o.device && stream == o.stream && split == o.split;
+  }
+};
+struct WorkspaceKeyHash {
+  size_t operator()(const WorkspaceKey &k) const {
+    return std::hash<const void *>()(k.stream) ^ (size_t(k.device) << 1) ^
+           size_t(k.split);
+  }
+};
 std::mutex g_ws_mutex;
-Workspace g_ws[64];
-// Library-owned per-device split-K scratch of the decode path: its counter
-// words are zero on allocation and every launch leaves them zero.
-Workspace g_split_ws[64];
+std::unordered_map<WorkspaceKey, Workspace, WorkspaceKeyHash> g_ws;
+std::vector<void *> g_ws_retired;
+
 
 // Makes `device` current for the scope and restores the caller's device.
 class DeviceScope {
@@ -92,6 +113,34 @@ ullm_status_t hip_fail(ullm_error_sink_t *sink, const char *what,
       return hip_fail(sink, what, e_);         \
     }                                          \
   } while (0)
+
+// The library-owned workspace of at least `need` bytes for this call
+// (zeroed when first allocated, for the split-K counters).  Allocates, so a
+// call that needs a larger buffer must not be under stream capture.
+ullm_status_t library_workspace(int device, const void *stream, bool split,
+                                uint64_t need, void **out,
+                                ullm_error_sink_t *error_sink) {
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  Workspace &cache = g_ws[WorkspaceKey{device, stream, split}];
+  if (cache.bytes < need) {
+    void *p = nullptr;
+    HIP_TRY(error_sink, "hipMalloc (workspace)", hipMalloc(&p, need));
+    if (split) {
+      const hipError_t e = hipMemset(p, 0, need);
+      if (e != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(error_sink, "hipMemset (workspace)", e);
+      }
+    }
+    if (cache.ptr != nullptr) {
+      g_ws_retired.push_back(cache.ptr);
+    }
+    cache.ptr = p;
+    cache.bytes = need;
+  }
+  *out = cache.ptr;
+  return ULLM_STATUS_OK;
+}
 
 ullm_status_t check_device(int device, ullm_error_sink_t *sink) {
   int count = 0;
@@ -698,23 +747,11 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
                                 "workspace needs " + std::to_string(need) + " bytes");
           }
         } else {
-          if (w->device >= 64) {
-            return write_error(error_sink, ULLM_STATUS_UNSUPPORTED,
-                               "library workspace supports device ordinals < 64");
+          const ullm_status_t st =
+              library_workspace(w->device, desc->stream, true, need, &ws, error_sink);
+          if (st != ULLM_STATUS_OK) {
+            return st;
           }
-          std::lock_guard<std::mutex> lock(g_ws_mutex);
-          Workspace &cache = g_split_ws[w->device];
-          if (cache.bytes < need) {
-            if (cache.ptr != nullptr) {
-              HIP_TRY(error_sink, "hipFree (workspace)", hipFree(cache.ptr));
-              cache.ptr = nullptr;
-              cache.bytes = 0;
-            }
-            HIP_TRY(error_sink, "hipMalloc (workspace)", hipMalloc(&cache.ptr, need));
-            cache.bytes = need;
-            HIP_TRY(error_sink, "hipMemset (workspace)", hipMemset(cache.ptr, 0, need));
-          }
-          ws = cache.ptr;
         }
         a.cnt = static_cast<uint32_t *>(ws);
         a.part = reinterpret_cast<float *>(static_cast<char *>(ws) +
@@ -748,22 +785,11 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
                               "workspace needs " + std::to_string(need) + " bytes");
         }
       } else {
-        if (w->device >= 64) {
-          return write_error(error_sink, ULLM_STATUS_UNSUPPORTED,
-                             "library workspace supports device ordinals < 64");
+        const ullm_status_t st =
+            library_workspace(w->device, desc->stream, false, need, &ws, error_sink);
+        if (st != ULLM_STATUS_OK) {
+          return st;
         }
-        std::lock_guard<std::mutex> lock(g_ws_mutex);
-        Workspace &cache = g_ws[w->device];
-        if (cache.bytes < need) {
-          if (cache.ptr != nullptr) {
-            HIP_TRY(error_sink, "hipFree (workspace)", hipFree(cache.ptr));
-            cache.ptr = nullptr;
-            cache.bytes = 0;
-          }
-          HIP_TRY(error_sink, "hipMalloc (workspace)", hipMalloc(&cache.ptr, need));
-          cache.bytes = need;
-        }
-        ws = cache.ptr;
       }
       uint8_t *wq = static_cast<uint8_t *>(ws);
       float *wsc = reinterpret_cast<float *>(wq + ullm::round_up(desc->m * w->k, 256));
