@@ -209,6 +209,17 @@ __device__ __forceinline__ i32x8 lds_operand(const char *p) {
   return __builtin_bit_cast(i32x8, v);
 }
 
+// Lane exchanges through DPP (no LDS crossbar, no lgkm wait): quad_perm
+// [1,0,3,2] swaps lanes across bit 0, [2,3,0,1] across bit 1, and row_ror:8
+// swaps the halves of each 16-lane row (lane ^ 8).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1, kDppXor2 = 0x4e, kDppXor8 = 0x128;
+
 // Four rows x one column per lane (an MFMA result) -> one row x four
 // columns: within each lane quad, lane q ends with row q of the quad's four
 // columns, in column order.  Two exchanges: across lane bit 1 (row pairs),
@@ -220,12 +231,12 @@ __device__ __forceinline__ f32x4 quad_transpose_f32(f32x4 v, uint32_t lane) {
   // values of those rows.
   const float k0 = b1 ? v[2] : v[0], k1 = b1 ? v[3] : v[1];
   const float s0 = b1 ? v[0] : v[2], s1 = b1 ? v[1] : v[3];
-  const float g0 = __shfl_xor(s0, 2, kWave), g1 = __shfl_xor(s1, 2, kWave);
+  const float g0 = dpp_f32<kDppXor2>(s0), g1 = dpp_f32<kDppXor2>(s1);
   // Keep row 2 b1 + b0 of columns c and c ^ 2; the partner c ^ 1 sends the
   // same row of columns c ^ 1 and c ^ 3.
   const float own = b0 ? k1 : k0, par = b0 ? g1 : g0;
-  const float r1 = __shfl_xor(b0 ? k0 : k1, 1, kWave);
-  const float r3 = __shfl_xor(b0 ? g0 : g1, 1, kWave);
+  const float r1 = dpp_f32<kDppXor1>(b0 ? k0 : k1);
+  const float r3 = dpp_f32<kDppXor1>(b0 ? g0 : g1);
   f32x4 out;
 #pragma unroll
   for (uint32_t c = 0; c < 4; ++c) {
@@ -426,11 +437,15 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t next = id + gridDim.x;
   const bool more = next < total;
   // The epilogue leaves the operand stages alone (its LDS chunk lies past
-  // them), so the next tile's first copies are issued before it.
-  if (more) {
-    setup(next);
-    prologue();
-  }
+  // them), so the next tile's first copies are issued during it: after the
+  // scales below are in use (waiting for them then does not wait for the
+  // copies) and before the stores.
+  auto issue_next = [&]() {
+    if (more) {
+      setup(next);
+      prologue();
+    }
+  };
 
   // Epilogue: lane holds rows 4 * (lane / 16) + r, column lane % 16 of each
   // 16 x 16 tile.  Scales are gathered first (independent loads in flight
@@ -523,7 +538,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
           f32x4 up;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            up[e] = __shfl_xor(t[e], 8, kWave);
+            up[e] = dpp_f32<kDppXor8>(t[e]);
             t[e] = silu_f32(t[e]) * up[e];
           }
           if (c4 < 8) {
@@ -534,6 +549,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
           *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 16 + c4) =
               pack_bf16x4(t);
         }
+      }
+      if (i == 0) {
+        issue_next();
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // this wave's chunk is written
 #pragma unroll
@@ -562,6 +580,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       // in-order LDS queue.
     }
   } else {
+    issue_next();
 #pragma unroll
     for (uint32_t i = 0; i < C::TM; ++i) {
 #pragma unroll
