@@ -165,8 +165,9 @@ struct GemmCfg {
   static constexpr uint32_t B_COPIES = (B_TILES + WAVES - 1) / WAVES;
   static constexpr bool B_EVEN = B_TILES % WAVES == 0;
   static_assert(A_TILES % WAVES == 0, "copy split");
-  // Epilogue staging of each wave's bf16 tile; rows padded by 16 bytes so
-  // the row groups of one LDS store land in different banks.
+  // Row pitch (bf16 elements) of a wave's epilogue chunk: a row of its
+  // tile, padded by 16 bytes so the rows of one LDS store land in different
+  // banks.
   static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
   // bf16 output is staged one 16-row m-tile per wave at a time, past the
   // operand stages, so the stages stay free for the next tile's copies.

@@ -1461,7 +1461,8 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
 // activation load then carries P blocks instead of one, which matters
 // because the texture path charges every activation load for 64 lanes
 // whether or not their rows exist (AQ4 M=8 14336->4096 on MI355X: 12.8 us
-// with four activation loads per group, 8.3 us with one).  The product of
+// with four activation loads per group, 8.3 us in a timing-only variant that
+// issued one).  The product of
 // register t with block P t + c's weights is valid only in class c's rows,
 // so the P block products go to separate accumulators p[c] and each lane
 // keeps the one of its own class (a lane's four accumulator rows lie in one
