@@ -1885,7 +1885,12 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //   deep K (< 384 stripes, K >= 8192): 16 waves, single stripes; AQ4 M=8
 //          14336->4096 13.0 against 14.3 us (11.7 with rows packed);
 //   small  (< 384 stripes, M <= 8, rows packed): 8 waves, single stripes;
-//          AQ4 M=8 4096->4096 4.9 against 5.3 us.
+//          AQ4 M=8 4096->4096 4.9 against 5.3 us;
+//   small, wide rows (< 384 stripes, AQ4 16 <= M <= 32, FP8 24 <= M <= 32):
+//          4 waves, single stripes; 4096->4096 AQ4 M=16 6.16 against 6.35,
+//          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
+//          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
+//          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
@@ -1905,11 +1910,15 @@ struct RsCfg {
 #ifndef ULLM_RS_SMALL
 #define ULLM_RS_SMALL 8, 1, 2, 1
 #endif
+#ifndef ULLM_RS_SMALL_WIDE
+#define ULLM_RS_SMALL_WIDE 4, 1, 2, 1
+#endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
+constexpr RsCfg kRsSmallWide{ULLM_RS_SMALL_WIDE};
 
 // Whether the multi-stripe kernel takes this launch.  It stages the
 // activation block once per workgroup and amortises it over a run of
@@ -1986,7 +1995,7 @@ hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
 // offsets for the weights and the activation block, and pays from M = 4 on
 // (below, the LDS-staged kernels stay ahead).  ULLM_GEMV_RS=0 disables it,
 // ULLM_GEMV_RS=1 forces it at any M.
-const RsCfg *plan_rs(const GemvArgs &a, bool vec) {
+const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
   static const int forced = env_int("ULLM_GEMV_RS", -1);
   const uint32_t rows = min(a.m, 32u);
   const uint32_t stripes = a.n16 / 16;
@@ -2000,6 +2009,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec) {
                    : stripes >= 384  ? &kRsMedium
                    : a.k >= 8192     ? &kRsDeepK
                    : a.m <= 8        ? &kRsSmall
+                   : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
                                      : nullptr;
   if (c == nullptr && forced == 1) {
     c = &kRsMedium;
@@ -2029,6 +2039,7 @@ hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
   return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
@@ -2038,6 +2049,7 @@ hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
   return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
@@ -2165,7 +2177,7 @@ hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
                                                  kRsSplit.depth, 1, EPI, true>, a, ks, s);
   }
   // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
-  if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec) : nullptr) {
+  if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec, false) : nullptr) {
     if (two) {
       return launch_fp8_rs<2, 1, EPI>(a, rs, s);
     }
@@ -2196,7 +2208,7 @@ hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
                : launch_split(aq4_gemv_rs_kernel<1, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
                                                  kRsSplit.depth, 1, EPI, true>, a, ks, s);
   }
-  if (const RsCfg *rs = plan_rs(a, vec)) {
+  if (const RsCfg *rs = plan_rs(a, vec, true)) {
     if (two) {
       return launch_aq4_rs<2, 1, EPI>(a, rs, s);
     }
