@@ -73,7 +73,7 @@ def test_aq4_quantize_export_dequant_bit_exact(uh, orc, gpu, n, k):
         and np.array_equal(z2, z_ref)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 7, 16, 17, 32, 33, 70])
+@pytest.mark.parametrize("m", [1, 2, 3, 7, 16, 17, 24, 27, 32, 33, 70])
 @pytest.mark.parametrize("n,k", [(17, 65), (64, 4096), (129, 640), (16, 4096)])
 def test_fp8_gemv_parity(uh, orc, gpu, m, n, k):
     w = weights(n, k, tag=3)
@@ -89,7 +89,7 @@ def test_fp8_gemv_parity(uh, orc, gpu, m, n, k):
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="fp8 gemv bf16")
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 7, 16, 17, 32, 33])
+@pytest.mark.parametrize("m", [1, 2, 3, 7, 9, 16, 20, 27, 32, 33])
 @pytest.mark.parametrize("n,k", [(17, 128), (64, 4096), (129, 640), (16, 1024)])
 def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
     w = weights(n, k, tag=5)
