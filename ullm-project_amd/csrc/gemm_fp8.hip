@@ -8,6 +8,7 @@
 // aligned activation rows (the prefill shapes), and a direct-from-L2 one that
 // loads operands straight from global memory in MFMA lane order for every
 // other shape.
+#include <algorithm>
 #include <cstdlib>
 
 #include "device_common.hpp"
@@ -666,6 +667,25 @@ hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
 }
 
 // Tuning override: ULLM_GEMM_CFG=mid selects the 128 x 128 block.
+// 128 x 128 blocks, two workgroups per CU, when the large blocks would
+// leave CUs idle: a round of them (two tiles per CU) takes ~0.82 of a round
+// of large blocks (their per-CU rate is ~0.7 of the large blocks', from
+// twice the operand traffic per flop), so they win whenever they need fewer
+// rounds.  Measured on MI355X, K = 4096 unless noted: M=2048 N=4096 52 ->
+// 39 us, N=4096 K=14336 139 -> 115 us, M=1024 N=4096 46 -> 33 us; N=6144
+// (one round of large blocks, two of mid) stays with the large blocks, 52
+// against 65 us.
+bool gemm_use_mid(uint32_t m, uint32_t n) {
+  static const uint32_t cus = gemm_cu_count();
+  const uint64_t mb = (m + 255) / 256;
+  const uint64_t t256 = mb * ((n + 255) / 256), t224 = mb * ((n + 223) / 224);
+  const uint64_t rounds_large =
+      std::min((t256 + cus - 1) / cus, (t224 + cus - 1) / cus);
+  const uint64_t tmid = uint64_t((m + 127) / 128) * ((n + 127) / 128);
+  const uint64_t rounds_mid = (tmid + 2 * cus - 1) / (2 * cus);
+  return double(rounds_mid) * 0.82 < double(rounds_large) * 0.95;
+}
+
 bool gemm_mid_forced() {
   static const bool v = [] {
     const char *e = std::getenv("ULLM_GEMM_CFG");
@@ -679,7 +699,7 @@ template <uint32_t EPI>
 hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
                   hipStream_t s) {
   if (vec && offsets_fit && a.k % 128 == 0 && a.m >= 128) {
-    if (gemm_mid_forced()) {
+    if (gemm_mid_forced() || gemm_use_mid(a.m, a.n)) {
       return launch_gemm_lds<GemmMid, EPI>(a, s);
     }
     return gemm_use_narrow(a.m, a.n) ? launch_gemm_lds<GemmNarrow, EPI>(a, s)
