@@ -609,7 +609,7 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 // any N with whole 224-column blocks) the tile count becomes a multiple of
 // the CU count where 256-column tiles leave the last round half empty.
 using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_BSTAGES>;
-using GemmMid = GemmCfg<128, 128, 2, 2>;    // 2 workgroups per CU
+using GemmMid = GemmCfg<128, 128, 2, 4>;    // 8 waves of 64 x 32; 2 workgroups per CU
 
 
 // Compute units of the current device.
@@ -668,13 +668,13 @@ hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
 
 // Tuning override: ULLM_GEMM_CFG=mid selects the 128 x 128 block.
 // 128 x 128 blocks, two workgroups per CU, when the large blocks would
-// leave CUs idle: a round of them (two tiles per CU) takes ~0.82 of a round
-// of large blocks (their per-CU rate is ~0.7 of the large blocks', from
-// twice the operand traffic per flop), so they win whenever they need fewer
-// rounds.  Measured on MI355X, K = 4096 unless noted: M=2048 N=4096 52 ->
-// 39 us, N=4096 K=14336 139 -> 115 us, M=1024 N=4096 46 -> 33 us; N=6144
-// (one round of large blocks, two of mid) stays with the large blocks, 52
-// against 65 us.
+// leave CUs idle: a round of them (two tiles per CU) takes ~0.8 of a round
+// of large blocks (their per-CU rate is ~0.7-0.75 of the large blocks',
+// from twice the operand traffic per flop), so they win whenever they need
+// fewer rounds.  Measured on MI355X, K = 4096 unless noted: M=2048 N=4096
+// 52 -> 37 us, N=4096 K=14336 139 -> 114 us, M=1024 N=4096 46 -> 30 us;
+// N=6144 (one round of large blocks, two of mid) stays with the large
+// blocks, 52-54 against 61 us.
 bool gemm_use_mid(uint32_t m, uint32_t n) {
   static const uint32_t cus = gemm_cu_count();
   const uint64_t mb = (m + 255) / 256;
