@@ -609,6 +609,9 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 // any N with whole 224-column blocks) the tile count becomes a multiple of
 // the CU count where 256-column tiles leave the last round half empty.
 using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_BSTAGES>;
+// 192 columns: 4 waves of 64 rows x 2 of 96 columns, for grids where it
+// fills the last round (M = 2048, N = 6144: 256 tiles, one full round).
+using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_BSTAGES>;
 using GemmMid = GemmCfg<128, 128, 2, 4>;    // 8 waves of 64 x 32; 2 workgroups per CU
 
 
@@ -627,20 +630,30 @@ uint32_t gemm_cu_count() {
 // each as long as one tile, and a tile's time scales with its width.  Pick
 // the 224-column block when that makes the rounds shorter overall.
 // ULLM_GEMM_BN=256/224 forces a width.
-bool gemm_use_narrow(uint32_t m, uint32_t n) {
+// Block width (256, 224 or 192 columns, 256 rows) whose rounds of
+// one-workgroup-per-CU tiles finish first: cost = rounds x width, ties to
+// the wider block.  ULLM_GEMM_BN forces one.
+uint32_t gemm_block_n(uint32_t m, uint32_t n) {
   static const int forced = [] {
     const char *e = std::getenv("ULLM_GEMM_BN");
     return e ? std::atoi(e) : 0;
   }();
-  if (forced == 256 || forced == 224) {
-    return forced == 224;
+  if (forced == 256 || forced == 224 || forced == 192) {
+    return uint32_t(forced);
   }
   static const uint32_t cus = gemm_cu_count();
   const uint64_t mb = (m + 255) / 256;
-  const uint64_t t256 = mb * ((n + 255) / 256), t224 = mb * ((n + 223) / 224);
-  const uint64_t cost256 = (t256 + cus - 1) / cus * 256;
-  const uint64_t cost224 = (t224 + cus - 1) / cus * 224;
-  return cost224 < cost256;
+  uint32_t best = 256;
+  uint64_t best_cost = ~uint64_t(0);
+  for (uint32_t bn : {256u, 224u, 192u}) {
+    const uint64_t tiles = mb * ((n + bn - 1) / bn);
+    const uint64_t cost = (tiles + cus - 1) / cus * bn;
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = bn;
+    }
+  }
+  return best;
 }
 
 template <class C, uint32_t EPI>
@@ -678,9 +691,11 @@ hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
 bool gemm_use_mid(uint32_t m, uint32_t n) {
   static const uint32_t cus = gemm_cu_count();
   const uint64_t mb = (m + 255) / 256;
-  const uint64_t t256 = mb * ((n + 255) / 256), t224 = mb * ((n + 223) / 224);
-  const uint64_t rounds_large =
-      std::min((t256 + cus - 1) / cus, (t224 + cus - 1) / cus);
+  uint64_t rounds_large = ~uint64_t(0);
+  for (uint32_t bn : {256u, 224u, 192u}) {
+    const uint64_t tiles = mb * ((n + bn - 1) / bn);
+    rounds_large = std::min(rounds_large, (tiles + cus - 1) / cus);
+  }
   const uint64_t tmid = uint64_t((m + 127) / 128) * ((n + 127) / 128);
   const uint64_t rounds_mid = (tmid + 2 * cus - 1) / (2 * cus);
   return double(rounds_mid) * 0.82 < double(rounds_large) * 0.95;
@@ -702,8 +717,11 @@ hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
     if (gemm_mid_forced() || gemm_use_mid(a.m, a.n)) {
       return launch_gemm_lds<GemmMid, EPI>(a, s);
     }
-    return gemm_use_narrow(a.m, a.n) ? launch_gemm_lds<GemmNarrow, EPI>(a, s)
-                                     : launch_gemm_lds<GemmLarge, EPI>(a, s);
+    switch (gemm_block_n(a.m, a.n)) {
+      case 224: return launch_gemm_lds<GemmNarrow, EPI>(a, s);
+      case 192: return launch_gemm_lds<GemmNarrow192, EPI>(a, s);
+      default: return launch_gemm_lds<GemmLarge, EPI>(a, s);
+    }
   }
   const dim3 grid((a.n + 63) / 64, (a.m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel<EPI>, grid, dim3(256), 0, s, a, vec);
