@@ -147,7 +147,8 @@ def test_residual_add_prefill_gemm(uh, orc, gpu):
 @pytest.mark.parametrize("m,n,k,rdtype,pad", [(300, 1000, 512, "f32", 0),
                                               (130, 37, 256, "bf16", 3),
                                               (257, 448, 384, "bf16", 0),
-                                              (256, 300, 256, "f32", 1)])
+                                              (256, 300, 256, "f32", 1),
+                                              (1024, 8448, 256, "bf16", 0)])
 def test_residual_add_prefill_gemm_bf16_out(uh, orc, gpu, m, n, k, rdtype, pad):
     """bf16 output through the staged GEMM epilogue: residual as 4-column
     vectors (aligned rows) or element by element (odd row strides), ragged

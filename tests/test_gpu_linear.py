@@ -281,7 +281,10 @@ def test_activation_quant_strided_view(uh, orc, gpu):
                                    (513, 1040, 1024),
                                    # 256 x 256 blocks fill one round exactly,
                                    # so the 256-column block is chosen
-                                   (256, 65536, 256)])
+                                   (256, 65536, 256),
+                                   # one round of 256 x 192 blocks beats the
+                                   # two rounds of 128 x 128 ones
+                                   (1024, 8448, 256)])
 def test_fp8_gemm_parity(uh, orc, gpu, m, n, k):
     w = weights(n, k, tag=13)
     q, s = orc.fp8_quantize_rows(w)
