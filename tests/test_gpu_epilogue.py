@@ -83,7 +83,7 @@ def test_silu_mul_decode(uh, orc, gpu, enc, m, f, k):
                  what=f"{enc} silu_mul bf16 {m}x{f}x{k}")
 
 
-@pytest.mark.parametrize("m,f,k", [(256, 1000, 512), (130, 37, 256)])
+@pytest.mark.parametrize("m,f,k", [(256, 1000, 512), (130, 37, 256), (40, 100, 256)])
 def test_silu_mul_prefill_gemm(uh, orc, gpu, m, f, k):
     w = weights(2 * f, k, tag=f)
     q, s = orc.fp8_quantize_rows(w)
@@ -148,7 +148,8 @@ def test_residual_add_prefill_gemm(uh, orc, gpu):
                                               (130, 37, 256, "bf16", 3),
                                               (257, 448, 384, "bf16", 0),
                                               (256, 300, 256, "f32", 1),
-                                              (1024, 8448, 256, "bf16", 0)])
+                                              (1024, 8448, 256, "bf16", 0),
+                                              (50, 300, 256, "bf16", 2)])
 def test_residual_add_prefill_gemm_bf16_out(uh, orc, gpu, m, n, k, rdtype, pad):
     """bf16 output through the staged GEMM epilogue: residual as 4-column
     vectors (aligned rows) or element by element (odd row strides), ragged

@@ -284,7 +284,11 @@ def test_activation_quant_strided_view(uh, orc, gpu):
                                    (256, 65536, 256),
                                    # one round of 256 x 192 blocks beats the
                                    # two rounds of 128 x 128 ones
-                                   (1024, 8448, 256)])
+                                   (1024, 8448, 256),
+                                   # M below one 128-row block: the LDS
+                                   # kernel with its single ragged block
+                                   (1, 300, 128), (33, 1000, 256),
+                                   (96, 4096, 512), (127, 520, 384)])
 def test_fp8_gemm_parity(uh, orc, gpu, m, n, k):
     w = weights(n, k, tag=13)
     q, s = orc.fp8_quantize_rows(w)

@@ -709,11 +709,14 @@ bool gemm_mid_forced() {
   return v;
 }
 
-// The epilogue kind is a template parameter of the kernels.
+// The epilogue kind is a template parameter of the kernels.  The LDS kernel
+// serves every M (rows past M are clamped on load and masked on store): at
+// K = 4096 it is 24 us against the direct kernel's 39 us for M = 32..96,
+// N = 4096, and 30 against 55-60 us at N = 28672.
 template <uint32_t EPI>
 hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
                   hipStream_t s) {
-  if (vec && offsets_fit && a.k % 128 == 0 && a.m >= 128) {
+  if (vec && offsets_fit && a.k % 128 == 0) {
     if (gemm_mid_forced() || gemm_use_mid(a.m, a.n)) {
       return launch_gemm_lds<GemmMid, EPI>(a, s);
     }
