@@ -11,7 +11,8 @@ holds back-to-back kernels with inputs already resident in HBM.  The kernel's
 average duration is timed with HIP events on the stream the kernels run on.
 
 Extra configurations (FP8 matvec, the small-M sweep, the M=2048 FP8 GEMM and
-the 32-layer AQ4 decode stack) are reported under "configs".  The CPU
+the 32-layer AQ4 decode stack; "gemm_shapes" adds the other prefill
+projections and M < 128) are reported under "configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
 
@@ -274,6 +275,14 @@ def main():
         configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
             r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
         log("gemm:", configs["fp8_gemm_m2048_k4096_n28672"])
+    if "gemm_shapes" in want:
+        # The other prefill projections, and M below one 128-row block.
+        for m, n, k in ((2048, 6144, 4096), (2048, 4096, 4096),
+                        (2048, 4096, 14336), (64, 4096, 4096),
+                        (64, 28672, 4096), (120, 14336, 4096)):
+            res = bench_gemm(r, m, n, k, max(3, args.steps // 10), 1)
+            configs[f"fp8_gemm_m{m}_k{k}_n{n}"] = res
+            log("gemm", m, n, k, res["us_per_launch"])
 
     cpu = cpu_baseline(args.cpu_seconds)
     us = head["us_per_launch"]
