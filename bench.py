@@ -10,9 +10,11 @@ Cache), captured once into a HIP graph and replayed, so that the timed region
 holds back-to-back kernels with inputs already resident in HBM.  The kernel's
 average duration is timed with HIP events on the stream the kernels run on.
 
-Extra configurations (FP8 matvec, the small-M sweep, the M=2048 FP8 GEMM and
-the 32-layer AQ4 decode stack; "gemm_shapes" adds the other prefill
-projections and M < 128) are reported under "configs".  The CPU
+Extra configurations (FP8 matvec, the FP8 small-M sweep M = 1..32 over the
+four Llama-3-8B layer shapes, a plain streaming-read floor at the headline
+sizes, the M=2048 FP8 GEMM and the 32-layer AQ4 decode stack; "gemm_shapes"
+adds the other prefill projections and M < 128) are reported under
+"configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
 
@@ -133,7 +135,10 @@ def bench_matvec(r, encoding, m, n, k, steps, warmup, seed=0):
 
 def bench_gemm(r, m, n, k, steps, warmup):
     torch, uh = r.torch, r.uh
-    ws = r.weights(uh.ENCODING_FP8_E4M3_ROW, n, k, 2, seed=3)
+    # At least 4 weight copies totalling more than 1 GB, so each call streams
+    # its weights from HBM rather than the 256 MB Infinity Cache.
+    copies = max(4, -(-ROTATE_BYTES // (n * k + 4 * n)))
+    ws = r.weights(uh.ENCODING_FP8_E4M3_ROW, n, k, copies, seed=3)
     g = torch.Generator(device=r.dev)
     g.manual_seed(11)
     x = torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16)
@@ -152,11 +157,33 @@ def bench_gemm(r, m, n, k, steps, warmup):
     _, us_e2e, _ = r.time_sweep(calls, steps, warmup)
     for w in ws:
         w.destroy()
-    return {"m": m, "n": n, "k": k, "us_per_launch": us_call,
+    return {"m": m, "n": n, "k": k, "copies": copies, "us_per_launch": us_call,
             "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
             "us_with_act_quant": us_e2e,
             "TFLOPS_with_act_quant": 2.0 * m * n * k / (us_e2e * 1e-6) / 1e12,
             "timing": mode}
+
+
+def bench_read_floor(r, nbytes, steps, warmup):
+    """A plain streaming read of `nbytes` per launch (torch's int32 sum) over
+    rotated random buffers totalling more than 1 GB, timed like the matvecs:
+    what a launch of that size costs with no unpacking or arithmetic."""
+    torch = r.torch
+    words = nbytes // 4
+    copies = max(4, -(-ROTATE_BYTES // nbytes))
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(99)
+    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (words,), generator=g,
+                          device=r.dev, dtype=torch.int32) for _ in range(copies)]
+    out = torch.empty((), dtype=torch.int64, device=r.dev)
+    calls = [(lambda b=b: torch.sum(b, out=out)) for b in bufs]
+    ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
+    del bufs
+    gbs = words * 4 / (us_call * 1e-6) / 1e9
+    return {"bytes_per_launch": words * 4, "copies": copies,
+            "us_per_launch": us_call, "GB_s": gbs,
+            "frac_hbm": gbs / HBM_PEAK_GBS, "timing": mode,
+            "kernel": "torch int32 sum (streaming read)"}
 
 
 def bench_stack(r, steps, warmup):
@@ -221,7 +248,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="aq4,fp8,gemm,stack")
+    ap.add_argument("--configs", default="aq4,fp8,sweep,floor,gemm,stack")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain 256 MiB torch copy (a known-size "
@@ -268,6 +295,13 @@ def main():
                                    max(10, args.steps // 5), 2)
                 configs[f"fp8_sweep_{name}_m{m}"] = res
                 log(name, m, res["GB_s"])
+    if "floor" in want:
+        for name, nbytes in (("aq4_m1_k4096_n14336", aq4_bytes(1, 14336, 4096)),
+                             ("fp8_m1_k4096_n4096", fp8_bytes(1, 4096, 4096)),
+                             ("fp8_m1_k14336_n4096", fp8_bytes(1, 4096, 14336))):
+            configs[f"read_floor_{name}"] = bench_read_floor(
+                r, nbytes, args.steps, args.warmup)
+            log("read floor", name, configs[f"read_floor_{name}"])
     if "stack" in want:
         configs["aq4_stack_32l_batch8"] = bench_stack(r, max(5, args.steps // 5), 2)
         log("stack:", configs["aq4_stack_32l_batch8"])

@@ -186,6 +186,25 @@ typedef struct ullm_linear_weight_export_desc_t {
   uint64_t reserved[4];
 } ullm_linear_weight_export_desc_t;
 
+/* Kernel families reported by ullm_linear_forward_plan. */
+#define ULLM_LINEAR_KERNEL_GEMV UINT32_C(1)        /* decode, bf16 activations */
+#define ULLM_LINEAR_KERNEL_GEMM_DIRECT UINT32_C(2) /* FP8 GEMM, operands from L2 */
+#define ULLM_LINEAR_KERNEL_GEMM_LDS UINT32_C(3)    /* FP8 GEMM, LDS-pipelined */
+
+/* The launch a forward call with a given descriptor makes (diagnostics: the
+ * parity tests use it to prove which kernel configuration they cover). */
+typedef struct ullm_linear_plan_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint32_t kernel;  /* ULLM_LINEAR_KERNEL_* (0 when M = 0: nothing runs) */
+  uint32_t block_m; /* GEMM: rows x columns of one output tile */
+  uint32_t block_n;
+  uint32_t tiles;   /* GEMM: output tiles */
+  uint32_t grid;    /* GEMM: workgroups; grid < tiles = persistent grid */
+  uint32_t split_k; /* GEMV: K parts per stripe group (1 = no split) */
+  uint64_t reserved[4];
+} ullm_linear_plan_t;
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -231,6 +250,21 @@ ULLM_HIP_API ullm_status_t ullm_linear_forward(
 ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
     const ullm_linear_forward_desc_t *desc, uint64_t *bytes,
     ullm_error_sink_t *error_sink);
+
+/* The kernel family and launch geometry ullm_linear_forward would use for
+ * this descriptor on the weight's device.  Launches nothing.  No counterpart
+ * in the reference: a diagnostic for parity tests and tuning reports. */
+ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
+    const ullm_linear_forward_desc_t *desc, ullm_linear_plan_t *plan,
+    ullm_error_sink_t *error_sink);
+
+/* Free every library-owned workspace of `device` (the buffers forward calls
+ * made with a null workspace, including those retired when a larger one
+ * replaced them), after waiting for the device.  HIP graphs captured with
+ * those buffers must not be replayed afterwards; later calls allocate anew.
+ * No counterpart in the reference. */
+ULLM_HIP_API ullm_status_t ullm_linear_release_workspaces(
+    int32_t device, ullm_error_sink_t *error_sink);
 
 /* Per-token E4M3 quantization of bf16 activations.  Stream-ordered. */
 ULLM_HIP_API ullm_status_t ullm_linear_quantize_activations(

@@ -70,3 +70,50 @@ def test_small_stack_chain(uh, orc, gpu, swiglu):
     st.destroy()
     assert torch.isfinite(logits.float()).all()
     assert 0.3 < float(h_final.float().pow(2).mean().sqrt()) < 3.0
+
+
+def test_full_shape_stack_chain(uh, orc, gpu):
+    """Config #5 at its real projection shapes (hidden 4096, qkv 6144, gate_up
+    28672, down 14336 -> 4096, lm_head 128256, batch 8), two layers: every
+    projection is checked against the oracle on the GPU's own input, with the
+    canonical AQ4 encoding read back from the device weight.  The 32-layer
+    benchmark repeats the same four launches per layer on other weights."""
+    import stack
+    layers = 2
+    st = stack.DecodeStack(uh, torch, gpu, batch=8, layers=layers, seed=11)
+    g = torch.Generator(device=gpu).manual_seed(12)
+    st.h0.copy_(torch.randn((8, stack.HIDDEN), generator=g, device=gpu))
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def check(lw, x_bits, y_gpu, alpha, what):
+        p, s, z = lw.export()
+        ref, _ = orc.aq4_gemv(np.ascontiguousarray(x_bits), p, s, z, alpha=alpha)
+        assert_close(y_gpu.float().cpu().numpy(), ref, bf16_out=True, what=what)
+
+    h = st.h0
+    for layer in range(layers):
+        w = st.weights[layer]
+        x0 = bits(h)
+        w["qkv"].forward(h, st.qkv_out, alpha=st.alpha_h)
+        check(w["qkv"], x0, st.qkv_out, st.alpha_h, f"qkv {layer}")
+        x1 = bits(st.qkv_out)[:, :stack.HIDDEN]
+        w["o"].forward(st.qkv_out[:, :stack.HIDDEN], st.o_out, alpha=st.alpha_h)
+        check(w["o"], x1, st.o_out, st.alpha_h, f"o {layer}")
+        x2 = bits(st.o_out)
+        w["gate_up"].forward(st.o_out, st.act, alpha=st.alpha_h)
+        check(w["gate_up"], x2, st.act, st.alpha_h, f"gate_up {layer}")
+        x3 = bits(st.act)[:, :stack.FFN]
+        w["down"].forward(st.act[:, :stack.FFN], st.h, alpha=st.alpha_f)
+        check(w["down"], x3, st.h, st.alpha_f, f"down {layer}")
+        h = st.h
+    x4 = bits(st.h)
+    st.lm_head.forward(st.h, st.logits, alpha=st.alpha_h)
+    check(st.lm_head, x4, st.logits, st.alpha_h, "lm_head")
+    logits = st.logits.clone()
+    st.step()
+    torch.cuda.synchronize()
+    assert torch.equal(st.logits, logits)
+    st.destroy()
+    assert 0.3 < float(logits.float().pow(2).mean().sqrt()) < 3.0

@@ -10,6 +10,9 @@
 // other shape.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -615,33 +618,11 @@ using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_BSTAGES>;
 using GemmMid = GemmCfg<128, 128, 2, 4>;    // 8 waves of 64 x 32; 2 workgroups per CU
 
 
-// Compute units of the current device.
-uint32_t gemm_cu_count() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-          hipSuccess || n <= 0) {
-    return 256;
-  }
-  return uint32_t(n);
-}
-
-// One workgroup per CU at a time: the kernel takes ceil(tiles / CUs) rounds,
-// each as long as one tile, and a tile's time scales with its width.  Pick
-// the 224-column block when that makes the rounds shorter overall.
-// ULLM_GEMM_BN=256/224 forces a width.
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
-// one-workgroup-per-CU tiles finish first: cost = rounds x width, ties to
-// the wider block.  ULLM_GEMM_BN forces one.
-uint32_t gemm_block_n(uint32_t m, uint32_t n) {
-  static const int forced = [] {
-    const char *e = std::getenv("ULLM_GEMM_BN");
-    return e ? std::atoi(e) : 0;
-  }();
-  if (forced == 256 || forced == 224 || forced == 192) {
-    return uint32_t(forced);
-  }
-  static const uint32_t cus = gemm_cu_count();
+// one-workgroup-per-CU tiles finish first: the kernel takes ceil(tiles /
+// CUs) rounds, each as long as one tile, and a tile's time scales with its
+// width, so cost = rounds x width, ties to the wider block.
+uint32_t gemm_block_n(uint32_t m, uint32_t n, uint32_t cus) {
   const uint64_t mb = (m + 255) / 256;
   uint32_t best = 256;
   uint64_t best_cost = ~uint64_t(0);
@@ -656,30 +637,6 @@ uint32_t gemm_block_n(uint32_t m, uint32_t n) {
   return best;
 }
 
-template <class C, uint32_t EPI>
-hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, int(C::LDS));
-  if (attr != hipSuccess) {
-    return attr;
-  }
-  const uint32_t tiles =
-      ((a.m + C::BM - 1) / C::BM) * ((a.n + C::BN - 1) / C::BN);
-  // One workgroup per CU (the LDS holds one), looping over tiles.
-  // ULLM_GEMM_PERSIST=0 launches one workgroup per tile instead.
-  static const bool persist = [] {
-    const char *e = std::getenv("ULLM_GEMM_PERSIST");
-    return e == nullptr || e[0] != '0';
-  }();
-  static const uint32_t cus = gemm_cu_count() * (C::LDS <= 80 * 1024 ? 2 : 1);
-  const uint32_t grid = persist && tiles > cus ? cus : tiles;
-  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(grid), dim3(C::WAVES * kWave),
-                     C::LDS, s, a);
-  return hipGetLastError();
-}
-
-// Tuning override: ULLM_GEMM_CFG=mid selects the 128 x 128 block.
 // 128 x 128 blocks, two workgroups per CU, when the large blocks would
 // leave CUs idle: a round of them (two tiles per CU) takes ~0.8 of a round
 // of large blocks (their per-CU rate is ~0.7-0.75 of the large blocks',
@@ -688,8 +645,7 @@ hipError_t launch_gemm_lds(const GemmArgs &a, hipStream_t s) {
 // 52 -> 37 us, N=4096 K=14336 139 -> 114 us, M=1024 N=4096 46 -> 30 us;
 // N=6144 (one round of large blocks, two of mid) stays with the large
 // blocks, 52-54 against 61 us.
-bool gemm_use_mid(uint32_t m, uint32_t n) {
-  static const uint32_t cus = gemm_cu_count();
+bool gemm_use_mid(uint32_t m, uint32_t n, uint32_t cus) {
   const uint64_t mb = (m + 255) / 256;
   uint64_t rounds_large = ~uint64_t(0);
   for (uint32_t bn : {256u, 224u, 192u}) {
@@ -701,30 +657,61 @@ bool gemm_use_mid(uint32_t m, uint32_t n) {
   return double(rounds_mid) * 0.82 < double(rounds_large) * 0.95;
 }
 
-bool gemm_mid_forced() {
-  static const bool v = [] {
-    const char *e = std::getenv("ULLM_GEMM_CFG");
-    return e != nullptr && e[0] == 'm';
-  }();
-  return v;
+template <class C>
+void fill_plan(GemmPlan &p, uint32_t m, uint32_t n, uint32_t cus,
+               bool persist) {
+  p.block_m = C::BM;
+  p.block_n = C::BN;
+  p.tiles = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
+  // One workgroup per CU (two for blocks whose LDS fits twice), looping
+  // over tiles.
+  const uint32_t slots = cus * (C::LDS <= 80 * 1024 ? 2 : 1);
+  p.grid = persist && p.tiles > slots ? slots : p.tiles;
 }
 
-// The epilogue kind is a template parameter of the kernels.  The LDS kernel
-// serves every M (rows past M are clamped on load and masked on store): at
-// K = 4096 it is 24 us against the direct kernel's 39 us for M = 32..96,
-// N = 4096, and 30 against 55-60 us at N = 28672.
+// Dynamic-LDS limit of a kernel raised once per (kernel, device).
+hipError_t raise_lds_limit(const void *kernel, uint32_t bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void *, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    return e;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kernel, dev}) != 0) {
+    return hipSuccess;
+  }
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          int(bytes));
+  if (e == hipSuccess) {
+    done.insert({kernel, dev});
+  }
+  return e;
+}
+
+template <class C, uint32_t EPI>
+hipError_t launch_gemm_lds(const GemmArgs &a, const GemmPlan &p,
+                           hipStream_t s) {
+  const void *k = reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI>);
+  const hipError_t attr = raise_lds_limit(k, C::LDS);
+  if (attr != hipSuccess) {
+    return attr;
+  }
+  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(p.grid),
+                     dim3(C::WAVES * kWave), C::LDS, s, a);
+  return hipGetLastError();
+}
+
 template <uint32_t EPI>
-hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
+hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
                   hipStream_t s) {
-  if (vec && offsets_fit && a.k % 128 == 0) {
-    if (gemm_mid_forced() || gemm_use_mid(a.m, a.n)) {
-      return launch_gemm_lds<GemmMid, EPI>(a, s);
-    }
-    switch (gemm_block_n(a.m, a.n)) {
-      case 224: return launch_gemm_lds<GemmNarrow, EPI>(a, s);
-      case 192: return launch_gemm_lds<GemmNarrow192, EPI>(a, s);
-      default: return launch_gemm_lds<GemmLarge, EPI>(a, s);
-    }
+  switch (p.kind) {
+    case kGemmMid: return launch_gemm_lds<GemmMid, EPI>(a, p, s);
+    case kGemmNarrow: return launch_gemm_lds<GemmNarrow, EPI>(a, p, s);
+    case kGemmNarrow192: return launch_gemm_lds<GemmNarrow192, EPI>(a, p, s);
+    case kGemmLarge: return launch_gemm_lds<GemmLarge, EPI>(a, p, s);
+    default: break;
   }
   const dim3 grid((a.n + 63) / 64, (a.m + 63) / 64);
   hipLaunchKernelGGL(fp8_gemm_direct_kernel<EPI>, grid, dim3(256), 0, s, a, vec);
@@ -732,6 +719,46 @@ hipError_t gemm_e(const GemmArgs &a, bool vec, bool offsets_fit,
 }
 
 }  // namespace
+
+// The LDS kernel serves every M (rows past M are clamped on load and masked
+// on store): at K = 4096 it is 24 us against the direct kernel's 39 us for
+// M = 32..96, N = 4096, and 30 against 55-60 us at N = 28672.  The direct
+// kernel takes unaligned activations, K not a multiple of 128, and offsets
+// past 32 bits.
+GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
+                       bool offsets_fit, uint32_t cus) {
+  GemmPlan p{};
+  if (!(vec && offsets_fit && k % 128 == 0)) {
+    p.kind = kGemmDirect;
+    p.block_m = 64;
+    p.block_n = 64;
+    p.tiles = ((m + 63) / 64) * ((n + 63) / 64);
+    p.grid = p.tiles;
+    return p;
+  }
+  // Tuning overrides (read only by a -DULLM_TUNING build): ULLM_GEMM_CFG=mid,
+  // ULLM_GEMM_BN=256/224/192, ULLM_GEMM_PERSIST=0 (one workgroup per tile).
+  const char *cfg = tuning_env("ULLM_GEMM_CFG");
+  const char *bn_env = tuning_env("ULLM_GEMM_BN");
+  const char *persist_env = tuning_env("ULLM_GEMM_PERSIST");
+  const bool persist = persist_env == nullptr || persist_env[0] != '0';
+  const int forced_bn = bn_env ? std::atoi(bn_env) : 0;
+  if ((cfg != nullptr && cfg[0] == 'm') ||
+      (forced_bn == 0 && gemm_use_mid(m, n, cus))) {
+    p.kind = kGemmMid;
+    fill_plan<GemmMid>(p, m, n, cus, persist);
+    return p;
+  }
+  const uint32_t bn = (forced_bn == 256 || forced_bn == 224 || forced_bn == 192)
+                          ? uint32_t(forced_bn)
+                          : gemm_block_n(m, n, cus);
+  switch (bn) {
+    case 224: p.kind = kGemmNarrow; fill_plan<GemmNarrow>(p, m, n, cus, persist); break;
+    case 192: p.kind = kGemmNarrow192; fill_plan<GemmNarrow192>(p, m, n, cus, persist); break;
+    default: p.kind = kGemmLarge; fill_plan<GemmLarge>(p, m, n, cus, persist); break;
+  }
+  return p;
+}
 
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            const ullm_linear_weight_t *w, uint32_t m, void *y,
@@ -756,10 +783,11 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
   const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
                            w->fp8.bytes() < (uint64_t(1) << 32);
+  const GemmPlan p = plan_fp8_gemm(m, a.n, a.k, vec, offsets_fit, device_cu_count());
   switch (epi.kind) {
-    case kEpiSiluMul: return gemm_e<kEpiSiluMul>(a, vec, offsets_fit, s);
-    case kEpiResidual: return gemm_e<kEpiResidual>(a, vec, offsets_fit, s);
-    default: return gemm_e<kEpiNone>(a, vec, offsets_fit, s);
+    case kEpiSiluMul: return gemm_e<kEpiSiluMul>(a, p, vec, s);
+    case kEpiResidual: return gemm_e<kEpiResidual>(a, p, vec, s);
+    default: return gemm_e<kEpiNone>(a, p, vec, s);
   }
 }
 

@@ -1720,7 +1720,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
 // stripe) with 4 once the grid has enough stripes to fill the chip.
 int pick_waves(bool aq4, uint64_t stripes, uint64_t mblocks, uint32_t units) {
   static const int forced = [] {
-    const char *e = std::getenv("ULLM_GEMV_WAVES");
+    const char *e = tuning_env("ULLM_GEMV_WAVES");
     return e ? std::atoi(e) : 0;
   }();
   if (forced == 2 || forced == 4 || forced == 8 || forced == 16) {
@@ -1736,7 +1736,7 @@ int pick_waves(bool aq4, uint64_t stripes, uint64_t mblocks, uint32_t units) {
 // Tuning override: ULLM_GEMV_LDS=0 disables the LDS-staged variant.
 bool lds_allowed() {
   static const bool ok = [] {
-    const char *e = std::getenv("ULLM_GEMV_LDS");
+    const char *e = tuning_env("ULLM_GEMV_LDS");
     return !(e && e[0] == '0');
   }();
   return ok;
@@ -1745,7 +1745,7 @@ bool lds_allowed() {
 // Tuning override: ULLM_GEMV_LDS_KB caps the staged activation block.
 uint32_t lds_cap(bool aq4) {
   static const uint32_t forced = [] {
-    const char *e = std::getenv("ULLM_GEMV_LDS_KB");
+    const char *e = tuning_env("ULLM_GEMV_LDS_KB");
     return e ? uint32_t(std::atoi(e)) * 1024u : 0u;
   }();
   const uint32_t cap = aq4 ? kXLdsBytesAq4 : kXLdsBytes;
@@ -1804,30 +1804,8 @@ hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-uint32_t cu_count() {
-  static std::mutex mu;
-  static std::unordered_map<int, uint32_t> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    return 256;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = cache.find(dev);
-  if (it != cache.end()) {
-    return it->second;
-  }
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-          hipSuccess || n <= 0) {
-    n = 256;
-  }
-  cache[dev] = uint32_t(n);
-  return uint32_t(n);
-}
-
 int env_int(const char *name, int dflt) {
-  const char *e = std::getenv(name);
+  const char *e = tuning_env(name);
   return e ? std::atoi(e) : dflt;
 }
 
@@ -1854,7 +1832,7 @@ uint32_t resident_blocks(Kernel kernel, uint32_t threads, uint32_t lds) {
           size_t(lds)) != hipSuccess || per_cu < 1) {
     per_cu = 1;
   }
-  const uint32_t n = cu_count() * uint32_t(per_cu);
+  const uint32_t n = device_cu_count() * uint32_t(per_cu);
   cache[key] = n;
   return n;
 }
@@ -1954,12 +1932,12 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   if (!aq4) {
     // ... and at M < 8 on grids of at most one stripe per CU (4096 -> 4096
     // M=1: 4.79 against 5.03 us).
-    return a.m >= 8 || stripes <= cu_count();
+    return a.m >= 8 || stripes <= device_cu_count();
   }
   // AQ4: runs of 3+ stripes at M >= 4, taking two resident workgroups per CU
   // when the activation block leaves room for two.
   const uint32_t per_cu = lds + 16u * 1024u <= 80u * 1024u ? 2u : 1u;
-  return a.m <= 2 || stripes >= 3 * cu_count() * per_cu;
+  return a.m <= 2 || stripes >= 3 * device_cu_count() * per_cu;
 }
 
 template <typename Kernel>
@@ -2080,7 +2058,7 @@ uint32_t plan_split(const GemvArgs &a, bool vec, uint32_t unit_k) {
     return 1;
   }
   const uint32_t G = (stripes + kRsSplit.s - 1) / kRsSplit.s;
-  uint32_t ks = forced > 1 ? uint32_t(forced) : (cu_count() + G - 1) / G;
+  uint32_t ks = forced > 1 ? uint32_t(forced) : (device_cu_count() + G - 1) / G;
   ks = std::min(ks, 16u);
   const uint32_t per = uint32_t(kRsSplit.waves * kRsSplit.batch);
   while (ks > 1 && a.units % (ks * per) != 0) {
@@ -2158,6 +2136,37 @@ bool x_vec_ok(const GemvArgs &a, uint32_t unit_k) {
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+uint32_t device_cu_count() {
+  static std::mutex mu;
+  static std::unordered_map<int, uint32_t> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) {
+    return it->second;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+          hipSuccess || n <= 0) {
+    n = 256;
+  }
+  cache[dev] = uint32_t(n);
+  return uint32_t(n);
+}
+
+const char *tuning_env(const char *name) {
+#ifdef ULLM_TUNING
+  return std::getenv(name);
+#else
+  (void)name;
+  return nullptr;
+#endif
+}
 
 template <int EPI>
 hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
@@ -2262,16 +2271,19 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
   }
 }
 
-uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4) {
+uint32_t gemv_split_parts(const GemvArgs &a, bool aq4) {
   if (aq4 ? a.m < 4 : a.m < 8) {
-    return 0;
+    return 1;
   }
   const bool vec = x_vec_ok(a, aq4 ? 128 : 64);
   if (!aq4 && use_ms(a, vec, a.m > 16 ? 2 : 1, false)) {
-    return 0;
+    return 1;
   }
-  GemvArgs probe = a;
-  const uint32_t ks = plan_split(probe, vec, aq4 ? 128 : 64);
+  return plan_split(a, vec, aq4 ? 128 : 64);
+}
+
+uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4) {
+  const uint32_t ks = gemv_split_parts(a, aq4);
   return ks > 1 ? split_bytes(a, ks) : 0;
 }
 

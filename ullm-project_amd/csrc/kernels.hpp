@@ -63,7 +63,36 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s);
 // Bytes of split-K scratch the launch for these arguments would use (0: it
 // does not split).  The first bytes are counters that must be zero.
 uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4);
+// K parts per stripe group that launch splits into (1: no split).
+uint32_t gemv_split_parts(const GemvArgs &a, bool aq4);
 // Offset of the partial sums inside that scratch.
 uint64_t gemv_scratch_part_offset(const GemvArgs &a);
+
+// ------------------------------------------------------------------ GEMM
+enum GemmKind : uint32_t {
+  kGemmDirect = 0,      // operands straight from L2, 64 x 64 blocks
+  kGemmLarge = 1,       // LDS-pipelined 256 x 256
+  kGemmNarrow = 2,      // LDS-pipelined 256 x 224
+  kGemmNarrow192 = 3,   // LDS-pipelined 256 x 192
+  kGemmMid = 4,         // LDS-pipelined 128 x 128, two workgroups per CU
+};
+struct GemmPlan {
+  uint32_t kind, block_m, block_n, tiles, grid;
+};
+// The kernel and grid launch_fp8_gemm takes for an M x N x K product on a
+// device of `cus` compute units (vec: activation rows 16-byte aligned;
+// offsets_fit: operand offsets below 2^32).  grid < tiles means a
+// persistent grid, each workgroup walking several tiles.
+GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
+                       bool offsets_fit, uint32_t cus);
+
+// ------------------------------------------------------------ host helpers
+// Compute units of the current device, looked up once per device.
+uint32_t device_cu_count();
+// Launch-plan overrides for tuning sweeps.  Only a library built with
+// -DULLM_TUNING reads them from the environment; the default build returns
+// null for every name, so the launchers always take the configurations the
+// parity tests cover.
+const char *tuning_env(const char *name);
 
 }  // namespace ullm

@@ -73,7 +73,7 @@ struct WorkspaceKeyHash {
 };
 std::mutex g_ws_mutex;
 std::unordered_map<WorkspaceKey, Workspace, WorkspaceKeyHash> g_ws;
-std::vector<void *> g_ws_retired;
+std::vector<std::pair<int, void *>> g_ws_retired;  // (device, buffer)
 
 
 // Makes `device` current for the scope and restores the caller's device.
@@ -116,24 +116,34 @@ ullm_status_t hip_fail(ullm_error_sink_t *sink, const char *what,
 
 // The library-owned workspace of at least `need` bytes for this call
 // (zeroed when first allocated, for the split-K counters).  Allocates, so a
-// call that needs a larger buffer must not be under stream capture.
+// call that needs a larger buffer is refused under stream capture.  The
+// zeroing is queued on the call's own stream, so the kernel that follows is
+// ordered after it even on a non-blocking stream.
 ullm_status_t library_workspace(int device, const void *stream, bool split,
                                 uint64_t need, void **out,
                                 ullm_error_sink_t *error_sink) {
   std::lock_guard<std::mutex> lock(g_ws_mutex);
   Workspace &cache = g_ws[WorkspaceKey{device, stream, split}];
   if (cache.bytes < need) {
+    const hipStream_t s = static_cast<hipStream_t>(const_cast<void *>(stream));
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(error_sink, "hipStreamIsCapturing", hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone) {
+      return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "the library-owned workspace must grow, which allocates: "
+                         "make this call once outside stream capture, or pass a workspace");
+    }
     void *p = nullptr;
     HIP_TRY(error_sink, "hipMalloc (workspace)", hipMalloc(&p, need));
     if (split) {
-      const hipError_t e = hipMemset(p, 0, need);
+      const hipError_t e = hipMemsetAsync(p, 0, need, s);
       if (e != hipSuccess) {
         (void)hipFree(p);
-        return hip_fail(error_sink, "hipMemset (workspace)", e);
+        return hip_fail(error_sink, "hipMemsetAsync (workspace)", e);
       }
     }
     if (cache.ptr != nullptr) {
-      g_ws_retired.push_back(cache.ptr);
+      g_ws_retired.emplace_back(device, cache.ptr);
     }
     cache.ptr = p;
     cache.bytes = need;
@@ -692,6 +702,68 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
   });
 }
 
+extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
+    const ullm_linear_forward_desc_t *desc, ullm_linear_plan_t *plan,
+    ullm_error_sink_t *error_sink) {
+  ULLM_ENTRY(error_sink, "forward plan", {
+    ullm_status_t st = validate_forward(desc, error_sink);
+    if (st != ULLM_STATUS_OK) {
+      return st;
+    }
+    st = ullm::validate_header(plan, error_sink, "plan output is null");
+    if (st != ULLM_STATUS_OK) {
+      return st;
+    }
+    if (!ullm::all_zero(plan->reserved)) {
+      return write_error(error_sink, ULLM_STATUS_RESERVED_NONZERO,
+                         "plan reserved fields must be zero");
+    }
+    plan->kernel = 0;
+    plan->block_m = plan->block_n = plan->tiles = plan->grid = 0;
+    plan->split_k = 1;
+    if (desc->m == 0) {
+      return ULLM_STATUS_OK;
+    }
+    const ullm_linear_weight_t *w = desc->weight;
+    DeviceScope scope(w->device);
+    HIP_TRY(error_sink, "hipSetDevice", scope.error());
+    const uint64_t ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
+    const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
+    if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 &&
+        desc->activation_mode == ULLM_LINEAR_ACT_EXACT) {
+      ullm::GemvArgs a{};
+      a.x = static_cast<const uint16_t *>(desc->x);
+      a.ldx = ldx;
+      a.m = static_cast<uint32_t>(desc->m);
+      a.n = static_cast<uint32_t>(w->n);
+      a.k = static_cast<uint32_t>(w->k);
+      a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
+      a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
+      plan->kernel = ULLM_LINEAR_KERNEL_GEMV;
+      plan->split_k = ullm::gemv_split_parts(a, !fp8w);
+      return ULLM_STATUS_OK;
+    }
+    // The prefill path quantizes into a dense [M][K] workspace; pre-quantized
+    // activations keep the caller's pointer and stride.
+    const bool prequant = desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN;
+    const uint64_t ldxq = prequant ? ldx : w->k;
+    const void *xq = prequant ? desc->x : desc->workspace;  // null: library-owned
+    const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
+    const bool offsets_fit = desc->m * ldxq < (uint64_t(1) << 32) &&
+                             w->fp8.bytes() < (uint64_t(1) << 32);
+    const ullm::GemmPlan p = ullm::plan_fp8_gemm(
+        static_cast<uint32_t>(desc->m), static_cast<uint32_t>(w->n),
+        static_cast<uint32_t>(w->k), vec, offsets_fit, ullm::device_cu_count());
+    plan->kernel = p.kind == ullm::kGemmDirect ? ULLM_LINEAR_KERNEL_GEMM_DIRECT
+                                               : ULLM_LINEAR_KERNEL_GEMM_LDS;
+    plan->block_m = p.block_m;
+    plan->block_n = p.block_n;
+    plan->tiles = p.tiles;
+    plan->grid = p.grid;
+    return ULLM_STATUS_OK;
+  });
+}
+
 extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
     const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink) {
   ULLM_ENTRY(error_sink, "linear forward", {
@@ -841,6 +913,42 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_quantize_activations(
                                    static_cast<uint8_t *>(desc->xq),
                                    desc->x_scales,
                                    static_cast<hipStream_t>(desc->stream)));
+    return ULLM_STATUS_OK;
+  });
+}
+
+extern "C" ULLM_HIP_API ullm_status_t ullm_linear_release_workspaces(
+    int32_t device, ullm_error_sink_t *error_sink) {
+  ULLM_ENTRY(error_sink, "release workspaces", {
+    const ullm_status_t st = check_device(device, error_sink);
+    if (st != ULLM_STATUS_OK) {
+      return st;
+    }
+    DeviceScope scope(device);
+    HIP_TRY(error_sink, "hipSetDevice", scope.error());
+    // Every stream of the device may still use a buffer.
+    HIP_TRY(error_sink, "hipDeviceSynchronize", hipDeviceSynchronize());
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    hipError_t first = hipSuccess;
+    for (auto it = g_ws.begin(); it != g_ws.end();) {
+      if (it->first.device == device) {
+        const hipError_t e = hipFree(it->second.ptr);
+        first = first == hipSuccess ? e : first;
+        it = g_ws.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    for (auto it = g_ws_retired.begin(); it != g_ws_retired.end();) {
+      if (it->first == device) {
+        const hipError_t e = hipFree(it->second);
+        first = first == hipSuccess ? e : first;
+        it = g_ws_retired.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    HIP_TRY(error_sink, "hipFree (workspace)", first);
     return ULLM_STATUS_OK;
   });
 }

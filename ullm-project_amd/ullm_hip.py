@@ -72,6 +72,9 @@ LAYOUT_GATED_PAIRS = 1
 EPILOGUE_NONE = 0
 EPILOGUE_SILU_MUL = 1
 EPILOGUE_RESIDUAL_ADD = 2
+KERNEL_GEMV = 1
+KERNEL_GEMM_DIRECT = 2
+KERNEL_GEMM_LDS = 3
 BACKEND_HIP = 1
 
 # ------------------------------------------------------------------- structs
@@ -128,6 +131,12 @@ class ForwardDesc(ctypes.Structure):
                 ("workspace_size", _u64), ("epilogue", _u32),
                 ("residual_dtype", _u32), ("residual", _vp),
                 ("residual_row_stride", _u64), ("reserved", _u64 * 1)]
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("kernel", _u32),
+                ("block_m", _u32), ("block_n", _u32), ("tiles", _u32),
+                ("grid", _u32), ("split_k", _u32), ("reserved", _u64 * 4)]
 
 
 class ActQuantDesc(ctypes.Structure):
@@ -208,6 +217,9 @@ _SIGNATURES = {
                                    ctypes.POINTER(ErrorSink)],
     "ullm_linear_quantize_activations": [ctypes.POINTER(ActQuantDesc),
                                          ctypes.POINTER(ErrorSink)],
+    "ullm_linear_forward_plan": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(Plan),
+                                 ctypes.POINTER(ErrorSink)],
+    "ullm_linear_release_workspaces": [_i32, ctypes.POINTER(ErrorSink)],
     "ullm_safetensors_open": [ctypes.POINTER(StOpenDesc), ctypes.POINTER(_vp),
                               ctypes.POINTER(ErrorSink)],
     "ullm_safetensors_close": [ctypes.POINTER(_vp), ctypes.POINTER(ErrorSink)],
@@ -447,6 +459,30 @@ class LinearWeight:
                                                 s.ref), s)
         return int(out.value)
 
+    def _forward_desc(self, x, y, *, x_scales, alpha, mode, stream, workspace,
+                      residual):
+        import torch
+        x_dtype = DTYPE_F8E4M3FN if x.dtype in (torch.uint8, torch.float8_e4m3fn) \
+            else DTYPE_BF16
+        epi = EPILOGUE_SILU_MUL if self.gated else EPILOGUE_NONE
+        res = {}
+        if residual is not None:
+            epi = EPILOGUE_RESIDUAL_ADD
+            res = dict(residual=_ptr(residual),
+                       residual_row_stride=residual.stride(0),
+                       residual_dtype=DTYPE_F32 if residual.dtype == torch.float32
+                       else DTYPE_BF16)
+        return new(ForwardDesc, weight=self.handle, m=x.shape[0], x=_ptr(x),
+                   x_row_stride=x.stride(0) if x.dim() == 2 else 0,
+                   x_scales=_ptr(x_scales), y=_ptr(y), y_row_stride=y.stride(0),
+                   x_dtype=x_dtype,
+                   y_dtype=DTYPE_F32 if y.dtype == torch.float32 else DTYPE_BF16,
+                   activation_mode=mode, alpha=alpha, stream=_stream(stream),
+                   workspace=_ptr(workspace),
+                   workspace_size=0 if workspace is None
+                   else workspace.numel() * workspace.element_size(),
+                   epilogue=epi, **res)
+
     def forward(self, x, y=None, *, x_scales=None, out_dtype=None, alpha=1.0,
                 mode=ACT_EXACT, stream=None, workspace=None, residual=None):
         """y = alpha * x @ W^T for x bf16 [M][>=K] (row stride honoured) or
@@ -458,28 +494,32 @@ class LinearWeight:
         if y is None:
             dt = out_dtype or torch.bfloat16
             y = torch.empty((m, self.n_out), dtype=dt, device=x.device)
-        x_dtype = DTYPE_F8E4M3FN if x.dtype in (torch.uint8, torch.float8_e4m3fn) \
-            else DTYPE_BF16
-        epi = EPILOGUE_SILU_MUL if self.gated else EPILOGUE_NONE
-        res = {}
-        if residual is not None:
-            epi = EPILOGUE_RESIDUAL_ADD
-            res = dict(residual=_ptr(residual),
-                       residual_row_stride=residual.stride(0),
-                       residual_dtype=DTYPE_F32 if residual.dtype == torch.float32
-                       else DTYPE_BF16)
-        d = new(ForwardDesc, weight=self.handle, m=m, x=_ptr(x),
-                x_row_stride=x.stride(0) if x.dim() == 2 else 0,
-                x_scales=_ptr(x_scales), y=_ptr(y), y_row_stride=y.stride(0),
-                x_dtype=x_dtype,
-                y_dtype=DTYPE_F32 if y.dtype == torch.float32 else DTYPE_BF16,
-                activation_mode=mode, alpha=alpha, stream=_stream(stream),
-                workspace=_ptr(workspace),
-                workspace_size=0 if workspace is None else workspace.numel() * workspace.element_size(),
-                epilogue=epi, **res)
+        d = self._forward_desc(x, y, x_scales=x_scales, alpha=alpha, mode=mode,
+                               stream=stream, workspace=workspace,
+                               residual=residual)
         s = _Sink()
         _check(lib().ullm_linear_forward(ctypes.byref(d), s.ref), s)
         return y
+
+    def plan(self, x, y, *, x_scales=None, alpha=1.0, mode=ACT_EXACT,
+             stream=None, workspace=None, residual=None) -> Plan:
+        """The launch forward() would make with these arguments
+        (ullm_linear_forward_plan); launches nothing."""
+        d = self._forward_desc(x, y, x_scales=x_scales, alpha=alpha, mode=mode,
+                               stream=stream, workspace=workspace,
+                               residual=residual)
+        out = new(Plan)
+        s = _Sink()
+        _check(lib().ullm_linear_forward_plan(ctypes.byref(d), ctypes.byref(out),
+                                              s.ref), s)
+        return out
+
+
+def release_workspaces(device: int = 0) -> None:
+    """Free the library-owned forward workspaces of a device
+    (ullm_linear_release_workspaces)."""
+    s = _Sink()
+    _check(lib().ullm_linear_release_workspaces(device, s.ref), s)
 
 
 def _addr(a):
