@@ -176,7 +176,7 @@ def bench_read_floor(r, nbytes, steps, warmup):
     bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (words,), generator=g,
                           device=r.dev, dtype=torch.int32) for _ in range(copies)]
     out = torch.empty((), dtype=torch.int64, device=r.dev)
-    calls = [(lambda b=b: torch.sum(b, out=out)) for b in bufs]
+    calls = [(lambda b=b: torch.sum(b, dim=0, out=out)) for b in bufs]
     ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
     del bufs
     gbs = words * 4 / (us_call * 1e-6) / 1e9

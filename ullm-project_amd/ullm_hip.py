@@ -139,6 +139,20 @@ class Plan(ctypes.Structure):
                 ("grid", _u32), ("split_k", _u32), ("reserved", _u64 * 4)]
 
 
+class EvidenceRequest(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("input", ctypes.c_void_p), ("input_size", _u64),
+                ("reserved", _u32 * 4)]
+
+
+class EvidenceResult(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32),
+                ("output_size", _u64), ("allocation_count", _u64),
+                ("copy_count", _u64), ("dispatch_count", _u64),
+                ("selected_backend", _u32), ("fallback_used", _u32),
+                ("terminal", _u32), ("reserved", _u32 * 4)]
+
+
 class ActQuantDesc(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("m", _u64),
                 ("k", _u64), ("x", _vp), ("x_row_stride", _u64), ("xq", _vp),
@@ -220,6 +234,11 @@ _SIGNATURES = {
     "ullm_linear_forward_plan": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(Plan),
                                  ctypes.POINTER(ErrorSink)],
     "ullm_linear_release_workspaces": [_i32, ctypes.POINTER(ErrorSink)],
+    "ullm_hip_evidence_submit": [ctypes.POINTER(EvidenceRequest), ctypes.POINTER(_vp),
+                                 ctypes.POINTER(ErrorSink)],
+    "ullm_hip_evidence_wait": [_vp, _u32, _vp, _u64, ctypes.POINTER(EvidenceResult),
+                               ctypes.POINTER(ErrorSink)],
+    "ullm_hip_evidence_destroy": [ctypes.POINTER(_vp), ctypes.POINTER(ErrorSink)],
     "ullm_safetensors_open": [ctypes.POINTER(StOpenDesc), ctypes.POINTER(_vp),
                               ctypes.POINTER(ErrorSink)],
     "ullm_safetensors_close": [ctypes.POINTER(_vp), ctypes.POINTER(ErrorSink)],
@@ -520,6 +539,102 @@ def release_workspaces(device: int = 0) -> None:
     (ullm_linear_release_workspaces)."""
     s = _Sink()
     _check(lib().ullm_linear_release_workspaces(device, s.ref), s)
+
+
+# ------------------------------------------------------------------ evidence
+EVIDENCE_ABI_VERSION = 1
+EVIDENCE_XOR = 0x5A
+
+
+def evidence_new(struct_type, **fields):
+    """An evidence struct with its {struct_size, abi_version} header."""
+    s = struct_type()
+    s.struct_size = ctypes.sizeof(struct_type)
+    s.abi_version = EVIDENCE_ABI_VERSION
+    for k, v in fields.items():
+        setattr(s, k, v)
+    return s
+
+
+class EvidenceCompletion:
+    """A submitted evidence transform (reference crates/ullm-hip/src/
+    lib.rs:293-375): wait() consumes it; dropping it destroys it."""
+
+    def __init__(self, handle: int, size: int):
+        self.handle = handle
+        self.size = size
+
+    def wait(self, output: bytearray, timeout_ms: int) -> dict:
+        if self.handle is None:
+            raise HipError(Status.HIP_INVALID_HANDLE,
+                           "evidence completion was already consumed")
+        handle, self.handle = self.handle, None
+        buf = (ctypes.c_uint8 * len(output)).from_buffer(output) if len(output) else None
+        res = evidence_new(EvidenceResult)
+        s = _Sink()
+        _check(lib().ullm_hip_evidence_wait(handle, min(int(timeout_ms), 2 ** 32 - 1),
+                                            ctypes.cast(buf, _vp) if buf is not None else None,
+                                            len(output), ctypes.byref(res), s.ref), s)
+        return {"output_size": res.output_size,
+                "allocation_count": res.allocation_count,
+                "copy_count": res.copy_count,
+                "dispatch_count": res.dispatch_count,
+                "selected_backend": res.selected_backend,
+                "fallback_used": bool(res.fallback_used),
+                "terminal": bool(res.terminal)}
+
+    def destroy(self):
+        if self.handle is None:
+            return
+        h = _vp(self.handle)
+        self.handle = None
+        lib().ullm_hip_evidence_destroy(ctypes.byref(h), None)
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def submit_evidence(data: bytes) -> EvidenceCompletion:
+    """Queue the XOR-0x5a evidence transform of ``data`` on the GPU
+    (reference lib.rs:377-406)."""
+    if len(data) == 0:
+        raise HipError(Status.INVALID_ARGUMENT, "evidence input must not be empty")
+    src = ctypes.create_string_buffer(bytes(data), len(data))
+    req = evidence_new(EvidenceRequest, input=ctypes.cast(src, _vp),
+                       input_size=len(data))
+    h = _vp()
+    s = _Sink()
+    _check(lib().ullm_hip_evidence_submit(ctypes.byref(req), ctypes.byref(h), s.ref), s)
+    if not h.value:
+        raise HipError(Status.INTERNAL_ERROR,
+                       "native evidence submit returned a null completion")
+    return EvidenceCompletion(h.value, len(data))
+
+
+def expected_evidence_output(data: bytes) -> bytes:
+    return bytes(b ^ EVIDENCE_XOR for b in data)
+
+
+def run_evidence(data: bytes, timeout_ms: int = 10000):
+    """Submit, wait and check the exact no-fallback byte contract
+    (reference lib.rs:408-441)."""
+    c = submit_evidence(data)
+    out = bytearray(len(data))
+    rep = c.wait(out, timeout_ms)
+    if rep["dispatch_count"] == 0:
+        raise HipError(Status.HIP_ZERO_DISPATCH,
+                       "evidence result contains zero kernel dispatches")
+    if (rep["selected_backend"] != BACKEND_HIP or rep["fallback_used"]
+            or not rep["terminal"] or rep["output_size"] != len(data)
+            or rep["allocation_count"] != 2 or rep["copy_count"] != 2
+            or rep["dispatch_count"] != 1
+            or bytes(out) != expected_evidence_output(data)):
+        raise HipError(Status.HIP_DISPATCH_CONTRACT,
+                       "evidence result failed the exact no-fallback byte contract")
+    return bytes(out), rep
 
 
 def _addr(a):
