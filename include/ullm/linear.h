@@ -258,6 +258,20 @@ ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
     const ullm_linear_forward_desc_t *desc, ullm_linear_plan_t *plan,
     ullm_error_sink_t *error_sink);
 
+/* ullm_linear_forward without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same descriptor, validation and result as ullm_linear_forward, except that
+ * desc->workspace must be null: all scratch comes from a fixed per-device
+ * array of 32 MiB held by the library for the life of the process (64 KiB of
+ * split-K counters plus 32 MiB - 64 KiB for split-K partials or the prefill
+ * path's quantized activations, M*K + 4*M bytes each rounded up to 256).
+ * Calls needing more are refused with ULLM_STATUS_UNSUPPORTED.  All calls on
+ * one device share that array: calls that overlap in time on one device
+ * (different streams or threads) race and must be ordered by the caller. */
+ULLM_HIP_API ullm_status_t ullm_linear_forward_noalloc(
+    const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink);
+
 /* Free every library-owned workspace of `device` (the buffers forward calls
  * made with a null workspace, including those retired when a larger one
  * replaced them), after waiting for the device.  HIP graphs captured with

@@ -20,7 +20,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "lib" / "libullm_hip.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["abi_v1.cpp", "linear_api.cpp", "safetensors.cpp", "evidence.hip", "weights.hip",
+SOURCES = ["abi_v1.cpp", "linear_api.cpp", "safetensors.cpp", "evidence.hip", "noalloc.hip", "weights.hip",
            "gemv.hip", "gemm_fp8.hip"]
 
 COMMON = [

@@ -8,6 +8,7 @@
 
 #include "device_common.hpp"
 #include "layout.hpp"
+#include "ullm/linear.h"
 
 namespace ullm {
 
@@ -87,6 +88,23 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
                        bool offsets_fit, uint32_t cus);
 
 // ------------------------------------------------------------ host helpers
+// Fixed device scratch of the allocation-free forward: a counter region
+// (zero, and left zero by every launch) and a data region.
+struct FixedScratch {
+  char *counters;
+  uint64_t counter_bytes;
+  char *base;
+  uint64_t bytes;
+};
+// Called with the weight's device current; fills *out or reports an error.
+typedef ullm_status_t (*FixedScratchFn)(int device, hipStream_t stream,
+                                        FixedScratch *out,
+                                        ullm_error_sink_t *sink);
+// ullm_linear_forward's body; `fixed` = null takes the caller's workspace or
+// the library-owned buffers.
+ullm_status_t forward_dispatch(const ullm_linear_forward_desc_t *desc,
+                               ullm_error_sink_t *sink, FixedScratchFn fixed);
+
 // Compute units of the current device, looked up once per device.
 uint32_t device_cu_count();
 // Launch-plan overrides for tuning sweeps.  Only a library built with

@@ -764,54 +764,86 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
   });
 }
 
-extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
-    const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink) {
-  ULLM_ENTRY(error_sink, "linear forward", {
-    const ullm_status_t st = validate_forward(desc, error_sink);
-    if (st != ULLM_STATUS_OK) {
-      return st;
-    }
-    if (desc->m == 0) {
-      return ULLM_STATUS_OK;
-    }
-    const ullm_linear_weight_t *w = desc->weight;
-    DeviceScope scope(w->device);
-    HIP_TRY(error_sink, "hipSetDevice", scope.error());
-    const hipStream_t s = static_cast<hipStream_t>(desc->stream);
-    const uint64_t ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
-    const uint64_t n_out = w->gate != 0 ? w->gate : w->n;
-    const uint64_t ldy = desc->y_row_stride ? desc->y_row_stride : n_out;
-    const bool y_f32 = desc->y_dtype == ULLM_LINEAR_DTYPE_F32;
-    const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
-    ullm::Epilogue epi{};
-    epi.kind = desc->epilogue == ULLM_LINEAR_EPILOGUE_SILU_MUL ? ullm::kEpiSiluMul
-               : desc->epilogue == ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD
-                   ? ullm::kEpiResidual
-                   : ullm::kEpiNone;
-    epi.n_out = static_cast<uint32_t>(n_out);
-    epi.res = desc->residual;
-    epi.ldr = desc->residual_row_stride ? desc->residual_row_stride : w->n;
-    epi.res_f32 = desc->residual_dtype == ULLM_LINEAR_DTYPE_F32;
+namespace ullm {
 
-    if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 &&
-        desc->activation_mode == ULLM_LINEAR_ACT_EXACT) {
-      ullm::GemvArgs a{};
-      a.tiles = w->tiles;
-      a.aux = w->aux;
-      a.x = static_cast<const uint16_t *>(desc->x);
-      a.y = desc->y;
-      a.ldx = ldx;
-      a.ldy = ldy;
-      a.m = static_cast<uint32_t>(desc->m);
-      a.n = static_cast<uint32_t>(w->n);
-      a.k = static_cast<uint32_t>(w->k);
-      a.alpha = desc->alpha;
-      a.y_f32 = y_f32;
-      a.epi = epi;
-      a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
-      a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
-      const uint64_t need = ullm::gemv_scratch_bytes(a, !fp8w);
-      if (need != 0) {
+// One forward call: validation, then the decode GEMV or the prefill GEMM.
+// Scratch (split-K counters and partials, quantized activations) comes from
+// the caller's workspace or the library-owned buffers, or, when `fixed` is
+// given, from the fixed scratch it returns for the weight's device (the
+// allocation-free entry point); then nothing is allocated.
+ullm_status_t forward_dispatch(const ullm_linear_forward_desc_t *desc,
+                               ullm_error_sink_t *error_sink,
+                               FixedScratchFn fixed) {
+  const ullm_status_t st = validate_forward(desc, error_sink);
+  if (st != ULLM_STATUS_OK) {
+    return st;
+  }
+  if (fixed != nullptr && desc->workspace != nullptr) {
+    return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                       "the allocation-free forward uses the library's fixed "
+                       "scratch: workspace must be null");
+  }
+  if (desc->m == 0) {
+    return ULLM_STATUS_OK;
+  }
+  const ullm_linear_weight_t *w = desc->weight;
+  DeviceScope scope(w->device);
+  HIP_TRY(error_sink, "hipSetDevice", scope.error());
+  const hipStream_t s = static_cast<hipStream_t>(desc->stream);
+  FixedScratch fs{};
+  if (fixed != nullptr) {
+    const ullm_status_t fst = fixed(w->device, s, &fs, error_sink);
+    if (fst != ULLM_STATUS_OK) {
+      return fst;
+    }
+  }
+  const uint64_t ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
+  const uint64_t n_out = w->gate != 0 ? w->gate : w->n;
+  const uint64_t ldy = desc->y_row_stride ? desc->y_row_stride : n_out;
+  const bool y_f32 = desc->y_dtype == ULLM_LINEAR_DTYPE_F32;
+  const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
+  ullm::Epilogue epi{};
+  epi.kind = desc->epilogue == ULLM_LINEAR_EPILOGUE_SILU_MUL ? ullm::kEpiSiluMul
+             : desc->epilogue == ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD
+                 ? ullm::kEpiResidual
+                 : ullm::kEpiNone;
+  epi.n_out = static_cast<uint32_t>(n_out);
+  epi.res = desc->residual;
+  epi.ldr = desc->residual_row_stride ? desc->residual_row_stride : w->n;
+  epi.res_f32 = desc->residual_dtype == ULLM_LINEAR_DTYPE_F32;
+
+  if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 &&
+      desc->activation_mode == ULLM_LINEAR_ACT_EXACT) {
+    ullm::GemvArgs a{};
+    a.tiles = w->tiles;
+    a.aux = w->aux;
+    a.x = static_cast<const uint16_t *>(desc->x);
+    a.y = desc->y;
+    a.ldx = ldx;
+    a.ldy = ldy;
+    a.m = static_cast<uint32_t>(desc->m);
+    a.n = static_cast<uint32_t>(w->n);
+    a.k = static_cast<uint32_t>(w->k);
+    a.alpha = desc->alpha;
+    a.y_f32 = y_f32;
+    a.epi = epi;
+    a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
+    a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
+    const uint64_t need = ullm::gemv_scratch_bytes(a, !fp8w);
+    if (need != 0) {
+      const uint64_t cnt_bytes = ullm::gemv_scratch_part_offset(a);
+      if (fixed != nullptr) {
+        // Counters in the fixed scratch's zeroed counter region (every
+        // launch leaves them zero), partials past it.
+        if (cnt_bytes > fs.counter_bytes || need - cnt_bytes > fs.bytes) {
+          return write_errorf(error_sink, ULLM_STATUS_UNSUPPORTED,
+                              "this call needs " + std::to_string(need) +
+                                  " bytes of split-K scratch; the fixed scratch holds " +
+                                  std::to_string(fs.bytes));
+        }
+        a.cnt = reinterpret_cast<uint32_t *>(fs.counters);
+        a.part = reinterpret_cast<float *>(fs.base);
+      } else {
         void *ws = desc->workspace;
         if (ws != nullptr) {
           if (desc->workspace_size < need) {
@@ -826,56 +858,72 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
           }
         }
         a.cnt = static_cast<uint32_t *>(ws);
-        a.part = reinterpret_cast<float *>(static_cast<char *>(ws) +
-                                           ullm::gemv_scratch_part_offset(a));
+        a.part = reinterpret_cast<float *>(static_cast<char *>(ws) + cnt_bytes);
       }
-      if (fp8w) {
-        a.n16 = static_cast<uint32_t>(w->fp8.n16);
-        a.units = static_cast<uint32_t>(w->fp8.blocks_per_stripe());
-        HIP_TRY(error_sink, "fp8 gemv kernel", ullm::launch_fp8_gemv(a, s));
-      } else {
-        a.n16 = static_cast<uint32_t>(w->aq4.n16);
-        a.units = static_cast<uint32_t>(w->aq4.groups);
-        HIP_TRY(error_sink, "aq4 gemv kernel", ullm::launch_aq4_gemv(a, s));
-      }
-      return ULLM_STATUS_OK;
     }
-
-    // FP8 activations on the FP8 matrix cores.
-    const uint8_t *xq = nullptr;
-    const float *xs = nullptr;
-    uint64_t ldxq = ldx;
-    if (desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN) {
-      xq = static_cast<const uint8_t *>(desc->x);
-      xs = desc->x_scales;
+    if (fp8w) {
+      a.n16 = static_cast<uint32_t>(w->fp8.n16);
+      a.units = static_cast<uint32_t>(w->fp8.blocks_per_stripe());
+      HIP_TRY(error_sink, "fp8 gemv kernel", ullm::launch_fp8_gemv(a, s));
     } else {
-      const uint64_t need = prefill_workspace_bytes(desc->m, w->k);
-      void *ws = desc->workspace;
-      if (ws != nullptr) {
-        if (desc->workspace_size < need) {
-          return write_errorf(error_sink, ULLM_STATUS_BUFFER_TOO_SMALL,
-                              "workspace needs " + std::to_string(need) + " bytes");
-        }
-      } else {
-        const ullm_status_t st =
-            library_workspace(w->device, desc->stream, false, need, &ws, error_sink);
-        if (st != ULLM_STATUS_OK) {
-          return st;
-        }
-      }
-      uint8_t *wq = static_cast<uint8_t *>(ws);
-      float *wsc = reinterpret_cast<float *>(wq + ullm::round_up(desc->m * w->k, 256));
-      HIP_TRY(error_sink, "activation quantize kernel",
-              ullm::launch_act_quant(static_cast<const uint16_t *>(desc->x), ldx,
-                                     desc->m, w->k, wq, wsc, s));
-      xq = wq;
-      xs = wsc;
-      ldxq = w->k;
+      a.n16 = static_cast<uint32_t>(w->aq4.n16);
+      a.units = static_cast<uint32_t>(w->aq4.groups);
+      HIP_TRY(error_sink, "aq4 gemv kernel", ullm::launch_aq4_gemv(a, s));
     }
-    HIP_TRY(error_sink, "fp8 gemm kernel",
-            ullm::launch_fp8_gemm(xq, xs, ldxq, w, static_cast<uint32_t>(desc->m),
-                                  desc->y, ldy, y_f32, desc->alpha, epi, s));
     return ULLM_STATUS_OK;
+  }
+
+  // FP8 activations on the FP8 matrix cores.
+  const uint8_t *xq = nullptr;
+  const float *xs = nullptr;
+  uint64_t ldxq = ldx;
+  if (desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN) {
+    xq = static_cast<const uint8_t *>(desc->x);
+    xs = desc->x_scales;
+  } else {
+    const uint64_t need = prefill_workspace_bytes(desc->m, w->k);
+    void *ws = desc->workspace;
+    if (fixed != nullptr) {
+      if (need > fs.bytes) {
+        return write_errorf(error_sink, ULLM_STATUS_UNSUPPORTED,
+                            "this call needs " + std::to_string(need) +
+                                " bytes of activation scratch; the fixed scratch holds " +
+                                std::to_string(fs.bytes));
+      }
+      ws = fs.base;
+    } else if (ws != nullptr) {
+      if (desc->workspace_size < need) {
+        return write_errorf(error_sink, ULLM_STATUS_BUFFER_TOO_SMALL,
+                            "workspace needs " + std::to_string(need) + " bytes");
+      }
+    } else {
+      const ullm_status_t st =
+          library_workspace(w->device, desc->stream, false, need, &ws, error_sink);
+      if (st != ULLM_STATUS_OK) {
+        return st;
+      }
+    }
+    uint8_t *wq = static_cast<uint8_t *>(ws);
+    float *wsc = reinterpret_cast<float *>(wq + ullm::round_up(desc->m * w->k, 256));
+    HIP_TRY(error_sink, "activation quantize kernel",
+            ullm::launch_act_quant(static_cast<const uint16_t *>(desc->x), ldx,
+                                   desc->m, w->k, wq, wsc, s));
+    xq = wq;
+    xs = wsc;
+    ldxq = w->k;
+  }
+  HIP_TRY(error_sink, "fp8 gemm kernel",
+          ullm::launch_fp8_gemm(xq, xs, ldxq, w, static_cast<uint32_t>(desc->m),
+                                desc->y, ldy, y_f32, desc->alpha, epi, s));
+  return ULLM_STATUS_OK;
+}
+
+}  // namespace ullm
+
+extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward(
+    const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink) {
+  ULLM_ENTRY(error_sink, "linear forward", {
+    return ullm::forward_dispatch(desc, error_sink, nullptr);
   });
 }
 

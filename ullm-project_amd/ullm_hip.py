@@ -234,6 +234,7 @@ _SIGNATURES = {
     "ullm_linear_forward_plan": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(Plan),
                                  ctypes.POINTER(ErrorSink)],
     "ullm_linear_release_workspaces": [_i32, ctypes.POINTER(ErrorSink)],
+    "ullm_linear_forward_noalloc": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(ErrorSink)],
     "ullm_hip_evidence_submit": [ctypes.POINTER(EvidenceRequest), ctypes.POINTER(_vp),
                                  ctypes.POINTER(ErrorSink)],
     "ullm_hip_evidence_wait": [_vp, _u32, _vp, _u64, ctypes.POINTER(EvidenceResult),
@@ -503,11 +504,14 @@ class LinearWeight:
                    epilogue=epi, **res)
 
     def forward(self, x, y=None, *, x_scales=None, out_dtype=None, alpha=1.0,
-                mode=ACT_EXACT, stream=None, workspace=None, residual=None):
+                mode=ACT_EXACT, stream=None, workspace=None, residual=None,
+                noalloc=False):
         """y = alpha * x @ W^T for x bf16 [M][>=K] (row stride honoured) or
         pre-quantized e4m3 (uint8) with x_scales.  A gated-pair weight returns
         silu(gate) * up (F columns); ``residual`` (bf16 or f32 [M][>=N], may
-        be ``y`` itself) is added to the product (ULLM_LINEAR_EPILOGUE_*)."""
+        be ``y`` itself) is added to the product (ULLM_LINEAR_EPILOGUE_*).
+        ``noalloc`` calls ullm_linear_forward_noalloc (scratch from the
+        library's fixed per-device array; ``workspace`` must be None)."""
         import torch
         m = x.shape[0]
         if y is None:
@@ -517,7 +521,8 @@ class LinearWeight:
                                stream=stream, workspace=workspace,
                                residual=residual)
         s = _Sink()
-        _check(lib().ullm_linear_forward(ctypes.byref(d), s.ref), s)
+        fn = lib().ullm_linear_forward_noalloc if noalloc else lib().ullm_linear_forward
+        _check(fn(ctypes.byref(d), s.ref), s)
         return y
 
     def plan(self, x, y, *, x_scales=None, alpha=1.0, mode=ACT_EXACT,
