@@ -165,25 +165,39 @@ def bench_gemm(r, m, n, k, steps, warmup):
 
 
 def bench_read_floor(r, nbytes, steps, warmup):
-    """A plain streaming read of `nbytes` per launch (torch's int32 sum) over
-    rotated random buffers totalling more than 1 GB, timed like the matvecs:
-    what a launch of that size costs with no unpacking or arithmetic."""
+    """A plain streaming read of `nbytes` per launch (libullm_bench.so's
+    stream_read_kernel: 16 KiB per wave, 16 loads in flight, XOR-folded)
+    over rotated random buffers totalling more than 1 GB, timed like the
+    matvecs: what a launch that reads that many bytes costs with no
+    unpacking or arithmetic."""
+    import ctypes
     torch = r.torch
-    words = nbytes // 4
+    bench_lib = ctypes.CDLL(str(ROOT / "ullm-project_amd" / "lib" / "libullm_bench.so"))
+    fn = bench_lib.ullm_bench_stream_read
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    nbytes = nbytes // 16 * 16
     copies = max(4, -(-ROTATE_BYTES // nbytes))
     g = torch.Generator(device=r.dev)
     g.manual_seed(99)
-    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (words,), generator=g,
+    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), generator=g,
                           device=r.dev, dtype=torch.int32) for _ in range(copies)]
-    out = torch.empty((), dtype=torch.int64, device=r.dev)
-    calls = [(lambda b=b: torch.sum(b, dim=0, out=out)) for b in bufs]
+    sink = torch.empty(((nbytes >> 17) + 1,), dtype=torch.int32, device=r.dev)
+
+    def call(b):
+        st = fn(b.data_ptr(), nbytes, sink.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"stream_read launch failed: {st}")
+
+    calls = [(lambda b=b: call(b)) for b in bufs]
     ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
     del bufs
-    gbs = words * 4 / (us_call * 1e-6) / 1e9
-    return {"bytes_per_launch": words * 4, "copies": copies,
+    gbs = nbytes / (us_call * 1e-6) / 1e9
+    return {"bytes_per_launch": nbytes, "copies": copies,
             "us_per_launch": us_call, "GB_s": gbs,
             "frac_hbm": gbs / HBM_PEAK_GBS, "timing": mode,
-            "kernel": "torch int32 sum (streaming read)"}
+            "kernel": "stream_read_kernel (plain streaming read)"}
 
 
 def bench_stack(r, steps, warmup):
@@ -302,6 +316,16 @@ def main():
             configs[f"read_floor_{name}"] = bench_read_floor(
                 r, nbytes, args.steps, args.warmup)
             log("read floor", name, configs[f"read_floor_{name}"])
+    if "stack_proj" in want:
+        # The stack's projections one at a time (AQ4, M = 8, contiguous x),
+        # over rotated copies like the headline.
+        for name, kk, nn in (("qkv", 4096, 6144), ("o", 4096, 4096),
+                             ("gate_up", 4096, 28672), ("down", 14336, 4096),
+                             ("lm_head", 4096, 128256)):
+            res = bench_matvec(r, uh.ENCODING_AQ4_G128, 8, nn, kk,
+                               max(10, args.steps // 5), 2)
+            configs[f"aq4_stack_{name}_m8"] = res
+            log("stack projection", name, res["us_per_launch"], res["GB_s"])
     if "stack" in want:
         configs["aq4_stack_32l_batch8"] = bench_stack(r, max(5, args.steps // 5), 2)
         log("stack:", configs["aq4_stack_32l_batch8"])

@@ -1,0 +1,337 @@
+//! Safe access to the quantized linear layer of the gfx950 library
+//! (include/ullm/linear.h), for crates/ullm-hip.
+//!
+//! Not compiled in this build's container (no Rust toolchain).  Wiring:
+//! `pub mod linear;` in crates/ullm-hip/src/lib.rs; this module uses that
+//! file's private helpers `sink`, `diagnostic`, `ensure_ok` and
+//! `ERROR_CAPACITY` (reference crates/ullm-hip/src/lib.rs:18,154-186), as
+//! `EvidenceCompletion` does (lib.rs:293-375).  The Python mirror
+//! ullm-project_amd/ullm_hip.py (`LinearWeight`, `forward`, `plan`) is the
+//! tested counterpart of every call here.
+//!
+//! Device memory is addressed by raw device pointers (`*const c_void`): the
+//! reference's TensorView carries metadata only (crates/ullm-core/src/
+//! tensor.rs:7-14), so buffers come from the caller's allocator.
+
+use std::ffi::c_void;
+use std::mem::size_of;
+use std::ptr::{self, NonNull};
+
+use ullm_hip_sys as sys;
+use sys::linear as ffi;
+
+use super::{diagnostic, ensure_ok, sink, HipError, Status, ERROR_CAPACITY};
+
+/// Weight encodings of the library (ULLM_LINEAR_ENCODING_*).
+#[derive(Clone, Copy, Debug, Eq, PartialEq)]
+pub enum WeightEncoding {
+    /// u8 E4M3FN codes [N][K] plus one f32 scale per row.
+    Fp8RowScaled,
+    /// Packed 4-bit codes [N][K/8] u32, f16 scale and zero per 128 k.
+    Aq4G128,
+}
+
+impl WeightEncoding {
+    const fn raw(self) -> u32 {
+        match self {
+            Self::Fp8RowScaled => ffi::ULLM_LINEAR_ENCODING_FP8_E4M3_ROW,
+            Self::Aq4G128 => ffi::ULLM_LINEAR_ENCODING_AQ4_G128,
+        }
+    }
+}
+
+/// Element types of activations and outputs.
+#[derive(Clone, Copy, Debug, Eq, PartialEq)]
+pub enum LinearDType {
+    Bf16,
+    F32,
+    F8E4M3Fn,
+}
+
+impl LinearDType {
+    const fn raw(self) -> u32 {
+        match self {
+            Self::Bf16 => ffi::ULLM_LINEAR_DTYPE_BF16,
+            Self::F32 => ffi::ULLM_LINEAR_DTYPE_F32,
+            Self::F8E4M3Fn => ffi::ULLM_LINEAR_DTYPE_F8E4M3FN,
+        }
+    }
+}
+
+/// A device-resident quantized weight; destroyed on drop.
+pub struct LinearWeight {
+    handle: NonNull<ffi::ullm_linear_weight_t>,
+    n: u64,
+    k: u64,
+    gated: bool,
+}
+
+// The native handle table is mutex-guarded and forward calls are
+// stream-ordered, so a weight may be shared across threads.
+unsafe impl Send for LinearWeight {}
+unsafe impl Sync for LinearWeight {}
+
+fn checked(raw: u32, buffer: &[u8; ERROR_CAPACITY], length: u64) -> Result<(), HipError> {
+    ensure_ok(raw, diagnostic(buffer, length))
+}
+
+impl LinearWeight {
+    /// Quantizes f32 weights [N][K] (device memory of `device`) on the GPU.
+    /// `gated`: a fused gate/up projection (N = 2F: F gate rows, F up rows).
+    pub fn quantize(
+        encoding: WeightEncoding,
+        n: u64,
+        k: u64,
+        device: i32,
+        values_f32: *const c_void,
+        gated: bool,
+        stream: *mut c_void,
+    ) -> Result<Self, HipError> {
+        let desc = ffi::ullm_linear_weight_desc_t {
+            struct_size: size_of::<ffi::ullm_linear_weight_desc_t>() as u32,
+            abi_version: sys::ULLM_HIP_ABI_VERSION,
+            encoding: encoding.raw(),
+            source: ffi::ULLM_LINEAR_SOURCE_F32,
+            n,
+            k,
+            memory: ffi::ULLM_MEMORY_DEVICE,
+            device,
+            values: values_f32,
+            scales: ptr::null(),
+            zeros: ptr::null(),
+            stream,
+            layout: if gated {
+                ffi::ULLM_LINEAR_LAYOUT_GATED_PAIRS
+            } else {
+                ffi::ULLM_LINEAR_LAYOUT_PLAIN
+            },
+            reserved0: 0,
+            reserved: [0; 3],
+        };
+        Self::create(&desc, gated)
+    }
+
+    /// Uploads canonical encoded host bytes: FP8 `values` u8 [N][K] and
+    /// `scales` f32 [N]; AQ4 `values` u32 [N][K/8], `scales` and `zeros`
+    /// f16 [N][K/128].
+    pub fn from_encoded_host(
+        encoding: WeightEncoding,
+        n: u64,
+        k: u64,
+        device: i32,
+        values: &[u8],
+        scales: &[u8],
+        zeros: Option<&[u8]>,
+        gated: bool,
+    ) -> Result<Self, HipError> {
+        let desc = ffi::ullm_linear_weight_desc_t {
+            struct_size: size_of::<ffi::ullm_linear_weight_desc_t>() as u32,
+            abi_version: sys::ULLM_HIP_ABI_VERSION,
+            encoding: encoding.raw(),
+            source: ffi::ULLM_LINEAR_SOURCE_ENCODED,
+            n,
+            k,
+            memory: ffi::ULLM_MEMORY_HOST,
+            device,
+            values: values.as_ptr().cast(),
+            scales: scales.as_ptr().cast(),
+            zeros: zeros.map_or(ptr::null(), |z| z.as_ptr().cast()),
+            stream: ptr::null_mut(),
+            layout: if gated {
+                ffi::ULLM_LINEAR_LAYOUT_GATED_PAIRS
+            } else {
+                ffi::ULLM_LINEAR_LAYOUT_PLAIN
+            },
+            reserved0: 0,
+            reserved: [0; 3],
+        };
+        Self::create(&desc, gated)
+    }
+
+    fn create(desc: &ffi::ullm_linear_weight_desc_t, gated: bool) -> Result<Self, HipError> {
+        let mut buffer = [0u8; ERROR_CAPACITY];
+        let mut error_sink = sink(&mut buffer);
+        let mut raw_handle = ptr::null_mut();
+        let raw = unsafe { ffi::ullm_linear_weight_create(desc, &mut raw_handle, &mut error_sink) };
+        checked(raw, &buffer, error_sink.message_length)?;
+        let handle = NonNull::new(raw_handle).ok_or_else(|| HipError::Status {
+            status: Status::InternalError,
+            message: "native weight create returned a null handle".to_owned(),
+        })?;
+        Ok(Self {
+            handle,
+            n: desc.n,
+            k: desc.k,
+            gated,
+        })
+    }
+
+    /// Output columns of a forward: N, or F = N / 2 for a gated pair.
+    pub fn output_columns(&self) -> u64 {
+        if self.gated {
+            self.n / 2
+        } else {
+            self.n
+        }
+    }
+
+    pub fn input_features(&self) -> u64 {
+        self.k
+    }
+
+    fn descriptor(&self, call: &Forward) -> ffi::ullm_linear_forward_desc_t {
+        let (epilogue, residual_dtype, residual, residual_row_stride) = match call.residual {
+            Some(r) => (
+                ffi::ULLM_LINEAR_EPILOGUE_RESIDUAL_ADD,
+                r.dtype.raw(),
+                r.ptr,
+                r.row_stride,
+            ),
+            None if self.gated => (ffi::ULLM_LINEAR_EPILOGUE_SILU_MUL, 0, ptr::null(), 0),
+            None => (ffi::ULLM_LINEAR_EPILOGUE_NONE, 0, ptr::null(), 0),
+        };
+        ffi::ullm_linear_forward_desc_t {
+            struct_size: size_of::<ffi::ullm_linear_forward_desc_t>() as u32,
+            abi_version: sys::ULLM_HIP_ABI_VERSION,
+            weight: self.handle.as_ptr(),
+            m: call.m,
+            x: call.x,
+            x_row_stride: call.x_row_stride,
+            x_scales: call.x_scales,
+            y: call.y,
+            y_row_stride: call.y_row_stride,
+            x_dtype: call.x_dtype.raw(),
+            y_dtype: call.y_dtype.raw(),
+            activation_mode: if call.fp8_prefill {
+                ffi::ULLM_LINEAR_ACT_FP8_PER_TOKEN
+            } else {
+                ffi::ULLM_LINEAR_ACT_EXACT
+            },
+            alpha: call.alpha,
+            stream: call.stream,
+            workspace: call.workspace,
+            workspace_size: call.workspace_size,
+            epilogue,
+            residual_dtype,
+            residual,
+            residual_row_stride,
+            reserved: [0; 1],
+        }
+    }
+
+    /// Y = alpha * X W^T (+ the epilogue), stream-ordered.
+    pub fn forward(&self, call: &Forward) -> Result<(), HipError> {
+        let desc = self.descriptor(call);
+        let mut buffer = [0u8; ERROR_CAPACITY];
+        let mut error_sink = sink(&mut buffer);
+        let raw = unsafe {
+            if call.no_alloc {
+                ffi::ullm_linear_forward_noalloc(&desc, &mut error_sink)
+            } else {
+                ffi::ullm_linear_forward(&desc, &mut error_sink)
+            }
+        };
+        checked(raw, &buffer, error_sink.message_length)
+    }
+
+    /// The kernel family and geometry `forward` would launch.
+    pub fn plan(&self, call: &Forward) -> Result<ffi::ullm_linear_plan_t, HipError> {
+        let desc = self.descriptor(call);
+        let mut plan = ffi::ullm_linear_plan_t {
+            struct_size: size_of::<ffi::ullm_linear_plan_t>() as u32,
+            abi_version: sys::ULLM_HIP_ABI_VERSION,
+            kernel: 0,
+            block_m: 0,
+            block_n: 0,
+            tiles: 0,
+            grid: 0,
+            split_k: 0,
+            reserved: [0; 4],
+        };
+        let mut buffer = [0u8; ERROR_CAPACITY];
+        let mut error_sink = sink(&mut buffer);
+        let raw = unsafe { ffi::ullm_linear_forward_plan(&desc, &mut plan, &mut error_sink) };
+        checked(raw, &buffer, error_sink.message_length).map(|()| plan)
+    }
+
+    /// Bytes of caller workspace `forward` needs (0 when none).
+    pub fn workspace_size(&self, call: &Forward) -> Result<u64, HipError> {
+        let desc = self.descriptor(call);
+        let mut bytes = 0u64;
+        let mut buffer = [0u8; ERROR_CAPACITY];
+        let mut error_sink = sink(&mut buffer);
+        let raw = unsafe { ffi::ullm_linear_workspace_size(&desc, &mut bytes, &mut error_sink) };
+        checked(raw, &buffer, error_sink.message_length).map(|()| bytes)
+    }
+}
+
+impl Drop for LinearWeight {
+    fn drop(&mut self) {
+        let mut raw_handle = self.handle.as_ptr();
+        let mut buffer = [0u8; ERROR_CAPACITY];
+        let mut error_sink = sink(&mut buffer);
+        let _ = unsafe { ffi::ullm_linear_weight_destroy(&mut raw_handle, &mut error_sink) };
+    }
+}
+
+/// A residual operand [M][N] of RESIDUAL_ADD (may alias `y`).
+#[derive(Clone, Copy, Debug)]
+pub struct Residual {
+    pub ptr: *const c_void,
+    pub dtype: LinearDType,
+    pub row_stride: u64,
+}
+
+/// The arguments of one forward call; device pointers of the weight's device.
+#[derive(Clone, Copy, Debug)]
+pub struct Forward {
+    pub m: u64,
+    pub x: *const c_void,
+    pub x_row_stride: u64,
+    pub x_dtype: LinearDType,
+    /// Per-token scales of pre-quantized E4M3 activations.
+    pub x_scales: *const f32,
+    pub y: *mut c_void,
+    pub y_row_stride: u64,
+    pub y_dtype: LinearDType,
+    pub alpha: f32,
+    /// bf16 activations quantized per token onto the FP8 matrix cores.
+    pub fp8_prefill: bool,
+    pub residual: Option<Residual>,
+    pub stream: *mut c_void,
+    pub workspace: *mut c_void,
+    pub workspace_size: u64,
+    /// Use ullm_linear_forward_noalloc (workspace must be null).
+    pub no_alloc: bool,
+}
+
+impl Forward {
+    /// bf16 X [M][K] -> bf16 Y [M][N], contiguous, on `stream`.
+    pub fn bf16(m: u64, x: *const c_void, y: *mut c_void, stream: *mut c_void) -> Self {
+        Self {
+            m,
+            x,
+            x_row_stride: 0,
+            x_dtype: LinearDType::Bf16,
+            x_scales: ptr::null(),
+            y,
+            y_row_stride: 0,
+            y_dtype: LinearDType::Bf16,
+            alpha: 1.0,
+            fp8_prefill: false,
+            residual: None,
+            stream,
+            workspace: ptr::null_mut(),
+            workspace_size: 0,
+            no_alloc: false,
+        }
+    }
+}
+
+/// Frees the library-owned forward workspaces of `device`.
+pub fn release_workspaces(device: i32) -> Result<(), HipError> {
+    let mut buffer = [0u8; ERROR_CAPACITY];
+    let mut error_sink = sink(&mut buffer);
+    let raw = unsafe { ffi::ullm_linear_release_workspaces(device, &mut error_sink) };
+    checked(raw, &buffer, error_sink.message_length)
+}

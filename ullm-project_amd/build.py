@@ -18,6 +18,10 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "lib" / "libullm_hip.so"
+# Measurement aid of bench.py (a streaming-read floor kernel); not linked
+# into the product library.
+BENCH_LIB = PKG / "lib" / "libullm_bench.so"
+BENCH_SOURCES = ["bench_read.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["abi_v1.cpp", "linear_api.cpp", "safetensors.cpp", "evidence.hip", "noalloc.hip", "weights.hip",
@@ -53,13 +57,15 @@ def build() -> Path:
     """Compile every source (always) and link libullm_hip.so."""
     BUILD.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC",
-           *map(str, objs), "-o", str(tmp)]
-    subprocess.run(cmd, check=True)
-    os.replace(tmp, LIB)
+    with ThreadPoolExecutor(max_workers=min(8, len(SOURCES) + len(BENCH_SOURCES))) as ex:
+        objs = list(ex.map(_compile, SOURCES + BENCH_SOURCES))
+    for lib, n in ((LIB, len(SOURCES)), (BENCH_LIB, None)):
+        parts = objs[:n] if n is not None else objs[len(SOURCES):]
+        tmp = lib.with_suffix(".so.tmp")
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC",
+               *map(str, parts), "-o", str(tmp)]
+        subprocess.run(cmd, check=True)
+        os.replace(tmp, lib)
     return LIB
 
 
