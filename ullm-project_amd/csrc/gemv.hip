@@ -1506,16 +1506,36 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
   const uint32_t rows = min(32u, a.m - m0);
   const __amdgpu_buffer_rsrc_t xbuf = byte_buffer(
       a.x + uint64_t(m0) * a.ldx, uint32_t(((rows - 1) * a.ldx + a.k) * 2));
-  // Lane l reads row m of its class and the 8 k of k-slot group l / 16 of
-  // its block (byte 64 c within the register's P-block span).
+  // MFMA lane 16 h + r takes A row r (row m of class c) and the 8 k of
+  // k-slot h of its block: 16 bytes at byte 64 c + 16 h of the register's
+  // P-block span, so an A row's four k-slots are one contiguous 64-byte run.
+  // The load itself assigns that run to the lane quad 4 r .. 4 r + 3 (lane
+  // 4 r + h reads k-slot h), which the texture path serves as one 64-byte
+  // access per quad instead of four (a quad of MFMA lanes spans four rows),
+  // and a lane permute (xperm) then hands each lane its MFMA operand.
+  // Measured on MI355X (TCP_TOTAL_CACHE_ACCESSES, AQ4 M=8 14336->4096):
+  // 64 accesses per activation load in MFMA order, against 16 for a
+  // contiguous kilobyte.
   uint32_t xoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = mt * 16 + (lane % 16) % RP;
-    const uint32_t c = (lane % 16) / RP;
-    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 8 * (lane / 16)) * 2 + 64 * c)
+    const uint32_t r = lane / 4, h = lane % 4;
+    const uint32_t m = mt * 16 + r % RP;
+    const uint32_t c = r / RP;
+    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 8 * h) * 2 + 64 * c)
                         : 0x80000000u;
   }
+  // Source lane of MFMA lane 16 h + r: 4 r + h (byte address for bpermute).
+  const int xsrc = int(((lane % 16) * 4 + lane / 16) * 4);
+  auto xperm = [&](bf16x8 v) {
+    u32x4 u = __builtin_bit_cast(u32x4, v);
+    u32x4 o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o[d] = uint32_t(__builtin_amdgcn_ds_bpermute(xsrc, int(u[d])));
+    }
+    return __builtin_bit_cast(bf16x8, o);
+  };
   // Class of this lane's accumulator rows 4 (l / 16) .. + 3.
   const uint32_t lcls = (lane / 16) * 4 / RP;
   const uint32_t wlane = lane * 16, zlane = (lane % 16) * 4;
@@ -1584,13 +1604,21 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
   auto consume = [&](const Batch &bt) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
+      bf16x8 xv[MT][XR];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int t = 0; t < XR; ++t) {
+          xv[mt][t] = xperm(bt.x[i][mt][t]);
+        }
+      }
       f32x4 xsum[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         xsum[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < XR; ++t) {
-          xsum[mt] = mfma_bf16(bt.x[i][mt][t], ones, xsum[mt]);
+          xsum[mt] = mfma_bf16(xv[mt][t], ones, xsum[mt]);
         }
       }
 #pragma unroll
@@ -1608,7 +1636,7 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_rs_kernel(
           const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][s][j], nmask, nmagic);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            p[j % P][mt] = mfma_bf16(bt.x[i][mt][j / P], bj, p[j % P][mt]);
+            p[j % P][mt] = mfma_bf16(xv[mt][j / P], bj, p[j % P][mt]);
           }
         }
         const float sf = f16_to_f32(uint16_t(bt.sz[i][s] & 0xffffu));
