@@ -1,12 +1,14 @@
-// bench_read.hip -- measurement aid for bench.py (libullm_bench.so): a plain
-// streaming read of a device buffer, the floor a kernel that must read every
-// byte of a weight matrix once cannot beat at that size.
+// bench_read.hip -- measurement aid for bench.py (libullm_bench.so): plain
+// streaming reads of a device buffer, the floor that a kernel which must read
+// every byte of a weight matrix once cannot beat at that size.
 //
-// Each wave reads a contiguous 16 KiB run of the buffer (16 independent
-// 1 KiB dwordx4 loads in flight per wave), XOR-folds it and writes one word
-// per workgroup, so no load can be optimised away.  One workgroup of 8 waves
-// covers 128 KiB; the grid covers the buffer.  Not part of the quantized
-// linear layer: it computes nothing the layer needs.
+// stream_read_kernel<W, D>: workgroups of W waves; each wave streams its own
+// contiguous `chunk` bytes as rounds of D independent 1 KiB loads (16 bytes
+// per lane, non-temporal), XOR-folds them and writes one word per wave only
+// when the fold hits a sentinel, so no load can be optimised away.  bench.py
+// times a few (W, D, chunk) shapes and reports the fastest: on MI355X the
+// best at 9-62 MB were 4 waves with 4-8 loads in flight over 4-8 KiB per
+// wave.  Not part of the quantized linear layer.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -14,49 +16,53 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr uint32_t kWaves = 8;
-constexpr uint32_t kLoads = 16;  // 1 KiB per wave per load
-constexpr uint64_t kWaveBytes = kLoads * 1024;
-constexpr uint64_t kBlockBytes = kWaves * kWaveBytes;
-
-__global__ __launch_bounds__(kWaves * 64) void stream_read_kernel(
-    const u32x4 *__restrict__ src, uint64_t vecs, uint32_t *__restrict__ sink) {
+template <int W, int D>
+__global__ __launch_bounds__(W * 64) void stream_read_kernel(
+    const u32x4 *__restrict__ src, uint64_t vecs, uint32_t chunk_vecs,
+    uint32_t *__restrict__ sink) {
   const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  const uint64_t base = (uint64_t(blockIdx.x) * kBlockBytes + wave * kWaveBytes) / 16;
+  const uint64_t base = (uint64_t(blockIdx.x) * W + wave) * chunk_vecs;
   u32x4 acc = {0u, 0u, 0u, 0u};
-  u32x4 v[kLoads];
+  for (uint32_t o = 0; o < chunk_vecs; o += D * 64) {
+    u32x4 v[D];
 #pragma unroll
-  for (uint32_t i = 0; i < kLoads; ++i) {
-    const uint64_t idx = base + i * 64 + lane;
-    v[i] = idx < vecs ? src[idx] : u32x4{0u, 0u, 0u, 0u};
-  }
+    for (int i = 0; i < D; ++i) {
+      const uint64_t idx = base + o + i * 64 + lane;
+      v[i] = idx < vecs ? __builtin_nontemporal_load(src + idx) : u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
-  for (uint32_t i = 0; i < kLoads; ++i) {
-    acc ^= v[i];
+    for (int i = 0; i < D; ++i) {
+      acc ^= v[i];
+    }
   }
-  uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
-  for (int off = 32; off > 0; off >>= 1) {
-    r ^= __shfl_xor(r, off);
+  const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (r == 0x9e3779b9u) {
+    sink[blockIdx.x * W + wave] = r;
   }
-  __shared__ uint32_t part[kWaves];
-  if (lane == 0) part[wave] = r;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t t = 0;
-    for (uint32_t w = 0; w < kWaves; ++w) t ^= part[w];
-    sink[blockIdx.x] = t;
-  }
+}
+
+template <int W, int D>
+int launch(const void *src, uint64_t bytes, uint32_t chunk, uint32_t *sink,
+           hipStream_t s) {
+  const uint64_t vecs = bytes / 16, cv = chunk / 16;
+  const uint64_t waves = (vecs + cv - 1) / cv;
+  const uint32_t blocks = uint32_t((waves + W - 1) / W);
+  hipLaunchKernelGGL((stream_read_kernel<W, D>), dim3(blocks), dim3(W * 64), 0, s,
+                     static_cast<const u32x4 *>(src), vecs, uint32_t(cv), sink);
+  return int(hipGetLastError());
 }
 
 }  // namespace
 
-// Reads `bytes` (a multiple of 16) at `src`; `sink` holds one u32 per
-// 128 KiB of input.  Returns the launch status.
+// Shape `shape` (0: 4 waves x 4 loads over 4 KiB per wave; 1: 4 x 8 over
+// 8 KiB; 2: 8 x 8 over 8 KiB) reads `bytes` (a multiple of 16) at `src`;
+// `sink` must hold one u32 per 4 KiB of input.  Returns the launch status.
 extern "C" __attribute__((visibility("default"))) int ullm_bench_stream_read(
-    const void *src, uint64_t bytes, uint32_t *sink, void *stream) {
-  const uint64_t blocks = (bytes + kBlockBytes - 1) / kBlockBytes;
-  hipLaunchKernelGGL(stream_read_kernel, dim3(uint32_t(blocks)), dim3(kWaves * 64), 0,
-                     static_cast<hipStream_t>(stream),
-                     static_cast<const u32x4 *>(src), bytes / 16, sink);
-  return int(hipGetLastError());
+    const void *src, uint64_t bytes, uint32_t shape, uint32_t *sink, void *stream) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (shape) {
+    case 0: return launch<4, 4>(src, bytes, 4096, sink, s);
+    case 1: return launch<4, 8>(src, bytes, 8192, sink, s);
+    default: return launch<8, 8>(src, bytes, 8192, sink, s);
+  }
 }

@@ -1264,14 +1264,61 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
   const uint32_t rows = min(32u, a.m - m0);
   const __amdgpu_buffer_rsrc_t xbuf = byte_buffer(
       a.x + uint64_t(m0) * a.ldx, uint32_t(((rows - 1) * a.ldx + a.k) * 2));
-  uint32_t xoff[MT];
+  // MFMA lane 16 h + r of register t takes A row r and the 16 bytes at
+  // chunk 2 h + t (P = 1; row r = m) or 2 h + c (P = 2; row r = 8 c + m) of
+  // the unit's 128-byte row segment.  The loads read whole row segments
+  // instead, 8 lanes per row (lane 8 m' + j reads chunk j of row m', rows
+  // 8 u .. 8 u + 7 in register u), so a lane quad reads one contiguous 64
+  // bytes, which the texture path serves as one access instead of four; a
+  // lane permute (xperm) then hands each lane its MFMA operand.
+  // The split-K launches (long K, 9 <= M <= 32) keep the MFMA-order loads:
+  // with two m-tiles the permutes cost more than they save there (MI355X,
+  // FP8 M=32 14336->4096: 2.33 against 2.53 TB/s).
+  constexpr bool XP = !SK;
+  uint32_t xoff[MT][XR];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = mt * 16 + (lane % 16) % RP;
-    const uint32_t c = (lane % 16) / RP;
-    xoff[mt] = m < rows ? uint32_t((m * a.ldx + 16 * (lane / 16)) * 2 + 16 * c)
-                        : 0x80000000u;
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+      if constexpr (XP) {
+        const uint32_t m = mt * 16 + 8 * u + lane / 8;
+        xoff[mt][u] = m < rows ? uint32_t((m * a.ldx) * 2 + 16 * (lane % 8))
+                               : 0x80000000u;
+      } else {
+        const uint32_t m = mt * 16 + (lane % 16) % RP;
+        const uint32_t c = (lane % 16) / RP;
+        xoff[mt][u] = m < rows ? uint32_t((m * a.ldx + 16 * (lane / 16)) * 2 +
+                                          16 * c + 16 * u)
+                               : 0x80000000u;
+      }
+    }
   }
+  // Source lane (bpermute byte address) of MFMA lane 16 h + r.
+  const uint32_t xh = lane / 16, xr = lane % 16;
+  const int xsrc0 = P == 2 ? int((8 * (xr % 8) + 2 * xh + xr / 8) * 4)
+                           : int((8 * (xr % 8) + 2 * xh) * 4);
+  const int xsrc1 = xsrc0 + 4;  // P = 1, register t = 1: chunk 2 h + 1
+  const bool xlo = xr < 8;      // P = 1: rows 0..7 come from register 0
+  auto xperm = [&](const bf16x8 (&v)[XR], int t) {
+    if constexpr (!XP) {
+      return v[t];
+    }
+    const int src = t == 0 ? xsrc0 : xsrc1;
+    u32x4 o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int lo = __builtin_amdgcn_ds_bpermute(
+          src, int(__builtin_bit_cast(u32x4, v[0])[d]));
+      if constexpr (XR == 2) {
+        const int hi = __builtin_amdgcn_ds_bpermute(
+            src, int(__builtin_bit_cast(u32x4, v[XR - 1])[d]));
+        o[d] = uint32_t(xlo ? lo : hi);
+      } else {
+        o[d] = uint32_t(lo);
+      }
+    }
+    return __builtin_bit_cast(bf16x8, o);
+  };
   const uint32_t lcls = (lane / 16) * 4 / RP;
   const uint32_t wlane = lane * 16, slane = (lane % 16) * 4;
 
@@ -1294,7 +1341,7 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
         for (int t = 0; t < XR; ++t) {
           bt.x[i][mt][t] = __builtin_bit_cast(
               bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                          xbuf, xoff[mt], ((lu + i) * 128 + t * 16) | xpast, 0));
+                          xbuf, xoff[mt][t], ((lu + i) * 128) | xpast, 0));
         }
       }
 #pragma unroll
@@ -1343,6 +1390,14 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
   auto consume = [&](const Batch &bt) {
 #pragma unroll
     for (int i = 0; i < B; ++i) {
+      bf16x8 xv[MT][XR];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int t = 0; t < XR; ++t) {
+          xv[mt][t] = xperm(bt.x[i][mt], t);
+        }
+      }
 #pragma unroll
       for (int s = 0; s < S; ++s) {
         const u32x4 wv = bt.w[i][s];
@@ -1356,9 +1411,8 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_rs_kernel(
             __builtin_bit_cast(bf16x8, u32x4{b45.x, b45.y, b67.x, b67.y});
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[s][mt][0] = mfma_bf16(bt.x[i][mt][0], w0, acc[s][mt][0]);
-          acc[s][mt][P - 1] =
-              mfma_bf16(bt.x[i][mt][XR - 1], w1, acc[s][mt][P - 1]);
+          acc[s][mt][0] = mfma_bf16(xv[mt][0], w0, acc[s][mt][0]);
+          acc[s][mt][P - 1] = mfma_bf16(xv[mt][XR - 1], w1, acc[s][mt][P - 1]);
         }
       }
     }
@@ -1919,6 +1973,16 @@ struct RsCfg {
 #ifndef ULLM_RS_SMALL_WIDE
 #define ULLM_RS_SMALL_WIDE 4, 1, 2, 1
 #endif
+// Stripe counts from which the medium tier takes over (build-time tuning).
+#ifndef ULLM_RS_MEDIUM_MIN
+#define ULLM_RS_MEDIUM_MIN 384u
+#endif
+#ifndef ULLM_RS_SMALL_MAX_M
+#define ULLM_RS_SMALL_MAX_M 0u
+#endif
+#ifndef ULLM_RS_MEDIUM_MIN_SMALL_M
+#define ULLM_RS_MEDIUM_MIN_SMALL_M 0u
+#endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
@@ -2012,7 +2076,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
   }
   const RsCfg *c = stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
-                   : stripes >= 384  ? &kRsMedium
+                   : stripes >= ULLM_RS_MEDIUM_MIN + (a.m <= ULLM_RS_SMALL_MAX_M ? ULLM_RS_MEDIUM_MIN_SMALL_M : 0u) ? &kRsMedium
                    : a.k >= 8192     ? &kRsDeepK
                    : a.m <= 8        ? &kRsSmall
                    : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
