@@ -1187,6 +1187,24 @@ __global__ __launch_bounds__(WAVES *kWave) void fp8_gemv_ms_kernel(
 // loaded with the system-coherent cache policy (sc0 sc1), which goes to
 // memory, and the counter is a device-scope atomic issued after this
 // workgroup's stores have completed.
+//
+// Why this is ordered without release/acquire fences (the gfx942/gfx950
+// memory model of the LLVM AMDGPU backend, which maps an agent-scope release
+// store to "buffer_wbl2 sc1; s_waitcnt vmcnt(0); store sc1" and an
+// agent-scope acquire load to "load sc1; s_waitcnt vmcnt(0); buffer_inv sc1"):
+//   * the L2 write-back of the release exists to push this XCD's dirty lines
+//     to memory; the partial sums are never dirty in L2, because sc0 sc1
+//     stores write through to memory, and s_waitcnt vmcnt(0) (below) returns
+//     only once every one of them is acknowledged by memory, which is the
+//     ordering the release's wait provides;
+//   * the agent-scope atomic (sc1) is performed at memory, after those
+//     acknowledgements, so the workgroup that reads count ks - 1 from it
+//     runs after every other workgroup's partial stores reached memory;
+//   * the L2 invalidate of the acquire exists so that later plain loads
+//     cannot hit stale lines of this XCD's L2; the finisher's partial loads
+//     are sc0 sc1 loads, which are served from memory, not from a possibly
+//     stale L2 line.
+// The finisher then adds the parts in k order, so results are deterministic.
 constexpr int kSc = 1 | 16;  // sc0 | sc1
 
 // Element i of the partial sums through a buffer descriptor over a.part
