@@ -1991,16 +1991,6 @@ struct RsCfg {
 #ifndef ULLM_RS_SMALL_WIDE
 #define ULLM_RS_SMALL_WIDE 4, 1, 2, 1
 #endif
-// Stripe counts from which the medium tier takes over (build-time tuning).
-#ifndef ULLM_RS_MEDIUM_MIN
-#define ULLM_RS_MEDIUM_MIN 384u
-#endif
-#ifndef ULLM_RS_SMALL_MAX_M
-#define ULLM_RS_SMALL_MAX_M 0u
-#endif
-#ifndef ULLM_RS_MEDIUM_MIN_SMALL_M
-#define ULLM_RS_MEDIUM_MIN_SMALL_M 0u
-#endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
@@ -2094,7 +2084,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
   }
   const RsCfg *c = stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
-                   : stripes >= ULLM_RS_MEDIUM_MIN + (a.m <= ULLM_RS_SMALL_MAX_M ? ULLM_RS_MEDIUM_MIN_SMALL_M : 0u) ? &kRsMedium
+                   : stripes >= 384  ? &kRsMedium
                    : a.k >= 8192     ? &kRsDeepK
                    : a.m <= 8        ? &kRsSmall
                    : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
