@@ -65,6 +65,8 @@ int main(void) {
   F(ullm_linear_forward_desc_t, residual_dtype) F(ullm_linear_forward_desc_t, residual)
   F(ullm_linear_forward_desc_t, residual_row_stride) F(ullm_linear_forward_desc_t, reserved)
   S(ullm_linear_act_quant_desc_t) F(ullm_linear_act_quant_desc_t, xq) F(ullm_linear_act_quant_desc_t, reserved)
+  S(ullm_linear_plan_t) F(ullm_linear_plan_t, kernel) F(ullm_linear_plan_t, grid) F(ullm_linear_plan_t, split_k)
+  F(ullm_linear_plan_t, reserved)
   S(ullm_linear_weight_export_desc_t) F(ullm_linear_weight_export_desc_t, values) F(ullm_linear_weight_export_desc_t, reserved)
   S(ullm_safetensors_open_desc_t) F(ullm_safetensors_open_desc_t, expected_sha256) F(ullm_safetensors_open_desc_t, reserved)
   S(ullm_safetensors_tensor_info_t) F(ullm_safetensors_tensor_info_t, shape) F(ullm_safetensors_tensor_info_t, offset)
@@ -97,6 +99,7 @@ def test_headers_compile_and_layout_matches_ctypes(uh, tmp_path):
         "ullm_linear_weight_desc_t": uh.WeightDesc, "ullm_linear_weight_info_t": uh.WeightInfo,
         "ullm_linear_forward_desc_t": uh.ForwardDesc,
         "ullm_linear_act_quant_desc_t": uh.ActQuantDesc,
+        "ullm_linear_plan_t": uh.Plan,
         "ullm_linear_weight_export_desc_t": uh.ExportDesc,
         "ullm_safetensors_open_desc_t": uh.StOpenDesc,
         "ullm_safetensors_tensor_info_t": uh.StTensorInfo,
@@ -318,3 +321,32 @@ def test_python_mirror_raises_without_gpu(uh):
     with pytest.raises(uh.HipError) as e:
         uh.LinearWeight.from_fp8(np.zeros((16, 64), np.uint8), np.ones(16, np.float32))
     assert e.value.status == uh.Status.HIP_UNAVAILABLE
+
+
+def test_plan_release_and_noalloc_entry_points_validate(uh):
+    """ullm_linear_forward_plan, ullm_linear_forward_noalloc and
+    ullm_linear_release_workspaces reject malformed calls before touching a
+    device, with the same statuses as ullm_linear_forward."""
+    lib = uh.lib()
+    bogus = ctypes.c_void_p(0x1234)
+    fwd = uh.new(uh.ForwardDesc, weight=bogus, m=1, x=0x10, y=0x20, alpha=1.0)
+    plan = uh.new(uh.Plan)
+    assert lib.ullm_linear_forward_plan(ctypes.byref(fwd), ctypes.byref(plan), None) \
+        == uh.Status.HIP_INVALID_HANDLE
+    assert lib.ullm_linear_forward_noalloc(ctypes.byref(fwd), None) \
+        == uh.Status.HIP_INVALID_HANDLE
+    assert lib.ullm_linear_forward_plan(None, ctypes.byref(plan), None) \
+        == uh.Status.INVALID_ARGUMENT
+    assert lib.ullm_linear_forward_noalloc(None, None) == uh.Status.INVALID_ARGUMENT
+    fwd.reserved[0] = 1
+    assert lib.ullm_linear_forward_noalloc(ctypes.byref(fwd), None) \
+        == uh.Status.RESERVED_NONZERO
+    s, buf = make_sink(uh, 256, abi_version=3)
+    assert lib.ullm_linear_forward_plan(ctypes.byref(fwd), ctypes.byref(plan),
+                                        ctypes.byref(s)) == uh.Status.INVALID_ABI_VERSION
+    if not uh.backend_probe()[0]:
+        s, buf = make_sink(uh)
+        assert lib.ullm_linear_release_workspaces(0, ctypes.byref(s)) \
+            == uh.Status.HIP_UNAVAILABLE
+        assert s.message_length > 0
+    assert ctypes.sizeof(uh.Plan) == 64
