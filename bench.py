@@ -13,8 +13,8 @@ average duration is timed with HIP events on the stream the kernels run on.
 Extra configurations (FP8 matvec, the FP8 small-M sweep M = 1..32 over the
 four Llama-3-8B layer shapes, a plain streaming-read floor at the headline
 sizes, the M=2048 FP8 GEMM and the 32-layer AQ4 decode stack; "gemm_shapes"
-adds the other prefill projections and M < 128) are reported under
-"configs".  The CPU
+adds the other prefill projections and M < 128, "vendor_gemm" the same FP8
+GEMM through hipBLASLt for reference) are reported under "configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
 
@@ -162,6 +162,34 @@ def bench_gemm(r, m, n, k, steps, warmup):
             "us_with_act_quant": us_e2e,
             "TFLOPS_with_act_quant": 2.0 * m * n * k / (us_e2e * 1e-6) / 1e12,
             "timing": mode}
+
+
+def bench_vendor_gemm(r, m, n, k, steps, warmup):
+    """The same FP8 GEMM through the vendor library (hipBLASLt via
+    torch._scaled_mm: E4M3 x E4M3 with per-tensor scales, bf16 out), over the
+    same number of rotated weight copies: a reference point for the FP8
+    matrix-core rate this part reaches on this shape.  Not a product path."""
+    torch = r.torch
+    copies = max(4, -(-ROTATE_BYTES // (n * k)))
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(17)
+    x = torch.randn((m, k), generator=g, device=r.dev).to(torch.float8_e4m3fn)
+    ws = [(torch.randn((n, k), generator=g, device=r.dev) * 8).to(torch.float8_e4m3fn)
+          for _ in range(copies)]
+    one = torch.ones((), dtype=torch.float32, device=r.dev)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=r.dev)
+
+    def call(w):
+        torch._scaled_mm(x, w.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16,
+                         out=y)
+
+    calls = [(lambda w=w: call(w)) for w in ws]
+    _, us_call, mode = r.time_sweep(calls, steps, warmup)
+    del ws
+    tflops = 2.0 * m * n * k / (us_call * 1e-6) / 1e12
+    return {"m": m, "n": n, "k": k, "copies": copies, "us_per_launch": us_call,
+            "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
+            "timing": mode, "library": "hipBLASLt via torch._scaled_mm"}
 
 
 def bench_read_floor(r, nbytes, steps, warmup):
@@ -344,6 +372,13 @@ def main():
         configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
             r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
         log("gemm:", configs["fp8_gemm_m2048_k4096_n28672"])
+    if "vendor_gemm" in want:
+        try:
+            configs["vendor_fp8_gemm_m2048_k4096_n28672"] = bench_vendor_gemm(
+                r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
+            log("vendor gemm:", configs["vendor_fp8_gemm_m2048_k4096_n28672"])
+        except Exception as exc:  # the vendor path is informational only
+            log(f"vendor gemm unavailable: {exc}")
     if "gemm_shapes" in want:
         # The other prefill projections, and M below one 128-row block.
         for m, n, k in ((2048, 6144, 4096), (2048, 4096, 4096),

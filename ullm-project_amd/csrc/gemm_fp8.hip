@@ -665,7 +665,15 @@ void fill_plan(GemmPlan &p, uint32_t m, uint32_t n, uint32_t cus,
   p.tiles = ((m + C::BM - 1) / C::BM) * ((n + C::BN - 1) / C::BN);
   // One workgroup per CU (two for blocks whose LDS fits twice), looping
   // over tiles.
-  const uint32_t slots = cus * (C::LDS <= 80 * 1024 ? 2 : 1);
+  uint32_t slots = cus * (C::LDS <= 80 * 1024 ? 2 : 1);
+  // Tuning override (read only by a -DULLM_TUNING build): ULLM_GEMM_GRID
+  // caps the persistent grid.
+  if (const char *g = tuning_env("ULLM_GEMM_GRID")) {
+    const int v = std::atoi(g);
+    if (v > 0 && uint32_t(v) < slots) {
+      slots = uint32_t(v);
+    }
+  }
   p.grid = persist && p.tiles > slots ? slots : p.tiles;
 }
 
