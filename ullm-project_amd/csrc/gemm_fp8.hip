@@ -144,9 +144,14 @@ typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 #endif
 
 template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_,
-          uint32_t BSTAGES_ = 2, uint32_t ASTAGES_ = 2>
+          uint32_t BSTAGES_ = 2, uint32_t ASTAGES_ = 2, bool PP_ = false>
 struct GemmCfg {
   static constexpr uint32_t BM = BM_, BN = BN_, BK = 128, WM = WM_, WN = WN_;
+  // Ping-pong main loop: the two halves of the waves (one wave of each per
+  // SIMD) alternate between reading their operands from LDS and running
+  // their MFMAs, so each SIMD's matrix core works while its other wave
+  // waits on LDS.
+  static constexpr bool PP = PP_;
   // A (activations, L2-resident) is double-buffered; B (weights, streamed
   // from HBM) may get a third buffer so its copies run two k-steps ahead.
   static constexpr uint32_t BSTAGES = BSTAGES_;
@@ -163,12 +168,14 @@ struct GemmCfg {
   static constexpr uint32_t A_BYTES = A_TILES * 1024;
   static constexpr uint32_t B_BYTES = B_TILES * 1024;
   static constexpr uint32_t STAGE_BYTES = ASTAGES * A_BYTES + BSTAGES * B_BYTES;
-  static constexpr uint32_t A_COPIES = A_TILES / WAVES;
+  // Waves issuing the global -> LDS copies (the first CW).
+  static constexpr uint32_t CW = PP ? WAVES / 2 : WAVES;
+  static constexpr uint32_t A_COPIES = A_TILES / CW;
   // B copies per wave; when the waves do not split B evenly, the last round
-  // of copies is done by the first B_TILES % WAVES waves only.
-  static constexpr uint32_t B_COPIES = (B_TILES + WAVES - 1) / WAVES;
-  static constexpr bool B_EVEN = B_TILES % WAVES == 0;
-  static_assert(A_TILES % WAVES == 0, "copy split");
+  // of copies is done by the first B_TILES % CW waves only.
+  static constexpr uint32_t B_COPIES = (B_TILES + CW - 1) / CW;
+  static constexpr bool B_EVEN = B_TILES % CW == 0;
+  static_assert(A_TILES % CW == 0, "copy split");
   // Row pitch (bf16 elements) of a wave's epilogue chunk: a row of its
   // tile, padded by 16 bytes so the rows of one LDS store land in different
   // banks.
@@ -189,6 +196,16 @@ __device__ __forceinline__ void dma16(const void *src, void *lds_wave_base) {
   __builtin_amdgcn_global_load_lds(
       (__attribute__((address_space(1))) void *)(src),
       (__attribute__((address_space(3))) void *)(lds_wave_base), 16, 0, 0);
+}
+
+// The same copy through a buffer resource: 32-bit lane offset, scalar
+// k-step offset, no 64-bit per-lane addresses held in registers.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc,
+                                          uint32_t voff, uint32_t soff,
+                                          void *lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void *)(lds_wave_base), 16,
+      voff, soff, 0, 0);
 }
 
 // Barrier without the fence of __syncthreads: LDS reads of this wave are
@@ -294,13 +311,13 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     // one chunk) land in 16 different bank groups.
 #pragma unroll
     for (uint32_t i = 0; i < C::A_COPIES; ++i) {
-      const uint32_t r = (i * C::WAVES + wave) * 8 + lane / 8;
+      const uint32_t r = (i * C::CW + wave % C::CW) * 8 + lane / 8;
       const uint32_t m = min(m0 + r, a.m - 1);
       aoff[i] = m * uint32_t(a.ldxq) + (((lane % 8) ^ ((r >> 1) & 7)) * 16);
     }
 #pragma unroll
     for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-      const uint32_t c = min(i * C::WAVES + wave, C::B_TILES - 1);
+      const uint32_t c = min(i * C::CW + wave % C::CW, C::B_TILES - 1);
       const uint32_t t = c / 2, kb = c % 2;
       const uint32_t T = min(T0 + t, stripes - 1);
       boff[i] = (T * a.units + kb) * 1024 + lane * 16;
@@ -311,24 +328,36 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   auto b_buf = [&](uint32_t ks) {
     return lds + C::ASTAGES * C::A_BYTES + (ks % C::BSTAGES) * C::B_BYTES;
   };
-  auto copy_a = [&](uint32_t ks) {
-    const uint8_t *abase = a.xq + uint64_t(ks) * C::BK;
-    char *st = a_buf(ks);
+  // Operand buffers (byte extents below 4 GiB: checked by the launcher).
+  const __amdgpu_buffer_rsrc_t abuf =
+      byte_buffer(a.xq, uint32_t(uint64_t(a.m) * a.ldxq));
+  const __amdgpu_buffer_rsrc_t bbuf =
+      byte_buffer(a.tiles, uint32_t(uint64_t(stripes) * a.units * 1024));
+  // With the ping-pong loop only the first CW waves copy.
+  const bool copier = !C::PP || wave < C::CW;
+  // Copies of step ks into the given stage (default: the ring slot of ks).
+  auto copy_a_to = [&](uint32_t ks, char *st) {
+    if (!copier) {
+      return;
+    }
 #pragma unroll
     for (uint32_t i = 0; i < C::A_COPIES; ++i) {
-      dma16(abase + aoff[i], st + (i * C::WAVES + wave) * 1024);
+      dma16_buf(abuf, aoff[i], ks * C::BK, st + (i * C::CW + wave) * 1024);
     }
   };
-  auto copy_b = [&](uint32_t ks) {
-    const uint8_t *bbase = a.tiles + uint64_t(ks) * 2048;
-    char *st = b_buf(ks);
+  auto copy_b_to = [&](uint32_t ks, char *st) {
+    if (!copier) {
+      return;
+    }
 #pragma unroll
     for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-      if (C::B_EVEN || i * C::WAVES + wave < C::B_TILES) {
-        dma16(bbase + boff[i], st + (i * C::WAVES + wave) * 1024);
+      if (C::B_EVEN || i * C::CW + wave < C::B_TILES) {
+        dma16_buf(bbuf, boff[i], ks * 2048, st + (i * C::CW + wave) * 1024);
       }
     }
   };
+  auto copy_a = [&](uint32_t ks) { copy_a_to(ks, a_buf(ks)); };
+  auto copy_b = [&](uint32_t ks) { copy_b_to(ks, b_buf(ks)); };
   constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
   constexpr uint32_t AAHEAD = C::ASTAGES - 1;  // k-steps A runs ahead
   auto prologue = [&]() {
@@ -374,6 +403,62 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   gemm_barrier();
 
+  if constexpr (C::PP) {
+    static_assert(AAHEAD == 1 && BAHEAD == 1 && C::WAVES == 8,
+                  "ping-pong: two stages, 8 waves");
+    // Waves 0-3 (group 0) and 4-7 (group 1) sit one of each per SIMD, and
+    // run the same loop -- read a step's operands from LDS, barrier, run
+    // its MFMAs, barrier -- with group 1 one phase behind (an extra barrier
+    // before its loop, matched by one after group 0's).  While one wave of
+    // a SIMD waits on LDS the other keeps the matrix core busy.  Group 0
+    // issues all copies: those for step ks + 1 go out before it reads step
+    // ks (their stage was last read by group 1 in the phase just ended)
+    // and are waited for before the barrier that ends its MFMA phase, so
+    // they have landed before either group reads them.
+    const bool g1 = wave >= C::WAVES / 2;
+    i32x8 af[C::TM], bf[C::TN];
+    if (g1) {
+      gemm_barrier();
+    }
+    // The stage being read, kept as a counter.
+    uint32_t st = 0;
+    char *const bstages = lds + C::ASTAGES * C::A_BYTES;
+#pragma clang loop unroll(disable)
+    for (uint32_t ks = 0; ks < ksteps; ++ks) {
+      if (ks + 1 < ksteps) {
+        copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
+        copy_b_to(ks + 1, bstages + (st ^ 1u) * C::B_BYTES);
+      }
+      const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
+      const char *Bs = bstages + st * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
+      st ^= 1u;
+#pragma unroll
+      for (uint32_t i = 0; i < C::TM; ++i) {
+        af[i] = a_operand(As, i);
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < C::TN; ++j) {
+        bf[j] = lds_operand(Bs + j * 2048);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      gemm_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (uint32_t i = 0; i < C::TM; ++i) {
+#pragma unroll
+        for (uint32_t j = 0; j < C::TN; ++j) {
+          acc[i][j] = mfma_fp8_k128(af[i], bf[j], acc[i][j]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's copies have landed
+      gemm_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!g1) {
+      gemm_barrier();
+    }
+  } else
   for (uint32_t ks = 0; ks < ksteps; ++ks) {
     // Copies needed by step ks + 1 are issued before those two steps
     // ahead: the in-order vector-memory counter then proves the former
@@ -426,7 +511,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     if constexpr (ahead2 > 0) {
       if (!two_more) {
         __builtin_amdgcn_s_waitcnt(0);
-      } else if (BAHEAD == 1 || C::B_EVEN || wave < C::B_TILES % C::WAVES) {
+      } else if (BAHEAD == 1 || C::B_EVEN || wave < C::B_TILES % C::CW) {
         wait_vm<ahead2>();
       } else {
         wait_vm<ahead2 - 1>();
@@ -608,14 +693,22 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
 }
 
 using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
-// 224 columns: 4 waves of 64 rows x 2 of 112 columns.  For N = 28672 (and
-// any N with whole 224-column blocks) the tile count becomes a multiple of
-// the CU count where 256-column tiles leave the last round half empty.
-using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_BSTAGES>;
-// 192 columns: 4 waves of 64 rows x 2 of 96 columns, for grids where it
-// fills the last round (M = 2048, N = 6144: 256 tiles, one full round).
-using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_BSTAGES>;
-using GemmMid = GemmCfg<128, 128, 2, 4>;    // 8 waves of 64 x 32; 2 workgroups per CU
+// 224 columns: 4 waves of 64 rows x 2 of 112 columns, ping-pong main loop.
+// For N = 28672 (and any N with whole 224-column blocks) the tile count
+// becomes a multiple of the CU count where 256-column tiles leave the last
+// round half empty.  Measured on MI355X at M=2048, N=28672: ping-pong
+// 215-220 against 232-235 us (per 128-deep k-step of every CU's tile 1.32
+// against 1.48-1.54 us, from a K sweep); a third B stage (B copies two
+// steps ahead) gained nothing.
+using GemmNarrow = GemmCfg<256, 224, 4, 2, 2, 2, true>;
+// 192 columns: 4 waves of 64 rows x 2 of 96 columns, ping-pong, for grids
+// where it fills the last round (M = 2048, N = 6144: 256 tiles, one full
+// round; 48.5 against 54.1 us without the ping-pong loop).
+using GemmNarrow192 = GemmCfg<256, 192, 4, 2, 2, 2, true>;
+// 8 waves of 64 x 32; 2 workgroups per CU.  The ping-pong loop measured
+// level or slower here (two workgroups already interleave on each SIMD)
+// and needs more than the 128 registers per wave two workgroups allow.
+using GemmMid = GemmCfg<128, 128, 2, 4>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
