@@ -144,6 +144,8 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     (6, 65600, 1024),    # AQ4 wide configuration at M = 6
     (8, 1000, 4096),     # AQ4 small grid: single stripes, 8 waves, packed
     (5, 300, 2048),      # AQ4 small grid, ragged last stripe
+    (8, 28672, 1024),    # 1792 stripes: AQ4 groups of 7 (7 per CU on 256 CUs)
+    (13, 28672, 1024),   # the same with a ragged 16-row tile
 ])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):

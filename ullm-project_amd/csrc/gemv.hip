@@ -1969,6 +1969,10 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
 //          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
 //          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
+//   seven per CU (AQ4, M <= 16, exactly 7 stripes per CU): 4 waves, groups
+//          of 7, one group per CU instead of 1.75 groups of 4; AQ4
+//          4096->28672 (1792 stripes on 256 CUs) M=8 14.8-15.3 against
+//          15.7-15.8 us, M=16 15.3-16.1 against 16.1-16.4 us.
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
@@ -1993,6 +1997,7 @@ struct RsCfg {
 #endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
+constexpr RsCfg kRsSeven{4, 1, 2, 7};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
@@ -2082,7 +2087,9 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
       (uint64_t(rows - 1) * a.ldx + a.k) * 2 >= (uint64_t(1) << 31)) {
     return nullptr;
   }
-  const RsCfg *c = stripes >= 4096   ? &kRsWide
+  const uint32_t cus = device_cu_count();
+  const RsCfg *c = aq4 && a.m <= 16 && stripes == 7 * cus ? &kRsSeven
+                   : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
                    : stripes >= 384  ? &kRsMedium
                    : a.k >= 8192     ? &kRsDeepK
@@ -2125,6 +2132,7 @@ template <int MT, int P, int EPI>
 hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
+  if (c == &kRsSeven) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSeven, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
   if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
