@@ -278,7 +278,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     GemmArgs a) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const uint32_t mblocks = (a.m + C::BM - 1) / C::BM;
   const uint32_t nblocks = (a.n + C::BN - 1) / C::BN;
   // A persistent grid walks tiles id = blockIdx.x + r * gridDim.x.  Tile ids
