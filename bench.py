@@ -370,12 +370,12 @@ def main():
         log("stack:", configs["aq4_stack_32l_batch8"])
     if "gemm" in want:
         configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
-            r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
+            r, 2048, 28672, 4096, max(5, args.steps // 5), 3)
         log("gemm:", configs["fp8_gemm_m2048_k4096_n28672"])
     if "vendor_gemm" in want:
         try:
             configs["vendor_fp8_gemm_m2048_k4096_n28672"] = bench_vendor_gemm(
-                r, 2048, 28672, 4096, max(3, args.steps // 10), 1)
+                r, 2048, 28672, 4096, max(5, args.steps // 5), 3)
             log("vendor gemm:", configs["vendor_fp8_gemm_m2048_k4096_n28672"])
         except Exception as exc:  # the vendor path is informational only
             log(f"vendor gemm unavailable: {exc}")
