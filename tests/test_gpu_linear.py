@@ -105,13 +105,16 @@ def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="aq4 gemv bf16")
 
 
-@pytest.mark.parametrize("m,n", [(1, 9000), (2, 9000), (3, 25000), (4, 25000),
-                                 (8, 12500), (16, 12500)])
+@pytest.mark.parametrize("m,n", [(1, 9000), (2, 9000), (1, 25000), (2, 25000),
+                                 (2, 13000), (3, 25000), (4, 25000), (8, 12500),
+                                 (16, 12500)])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     """Enough 16-row stripes (the last one ragged) that the launcher gives each
     workgroup of the multi-stripe kernels a run of three or more stripes (at
-    M >= 4, on a 256-CU device); K = 4096 as in the Llama shapes."""
+    M >= 4, on a 256-CU device; AQ4 M = 1 at 1563 stripes and M = 2 at 813
+    or more take the whole-stripes-per-wave configuration); K = 4096 as in
+    the Llama shapes."""
     k = 4096
     w = weights(n, k, tag=21)
     xb = activations_bf16(orc, m, k, tag=m + 200)

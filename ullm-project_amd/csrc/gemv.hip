@@ -1949,6 +1949,14 @@ struct MsCfg {
   int waves, batch, depth, ks;  // ks: waves splitting one stripe's K
 };
 constexpr MsCfg kAq4Ms{ULLM_AQ4_MS_CFG};
+// AQ4 at M <= 2 with 6 (M = 1) or 3 (M = 2) to 16 stripes per CU: 4 waves,
+// each owning whole stripes (no cross-wave reduction), 4 groups per batch.
+// Measured on MI355X (K = 4096): M=1 4096->28672 12.7-12.8 against 14.6 us,
+// M=2 4096->14336 8.2 against 9.1 us; M=1 4096->14336 (3.5 stripes per CU)
+// level (7.65 against 7.68 us, kept on the default); behind at 1.5 and 31
+// stripes per CU (M=1 4096->6144 6.8 against 5.0 us, 4096->128256 51-53
+// against 46-48 us).
+constexpr MsCfg kAq4MsWhole{4, 4, 2, 1};
 constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 
 // Register-staged kernel configurations by grid size (measured on MI355X,
@@ -2060,6 +2068,15 @@ hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
 
 template <int MT, int NR, int P, int EPI>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
+  if constexpr (MT == 1) {
+    const uint32_t stripes = a.n16 / 16, cus = device_cu_count();
+    if (a.m <= 2 && stripes >= (a.m == 1 ? 6 : 3) * cus && stripes < 16 * cus &&
+        a.units % uint32_t(kAq4MsWhole.batch) == 0) {
+      constexpr MsCfg c = kAq4MsWhole;
+      return launch_ms(aq4_gemv_ms_kernel<MT, c.waves, c.ks, c.batch, c.depth, NR, P, EPI>,
+                       a, c.waves, ms_lds_bytes(a, true), s, c.waves / c.ks);
+    }
+  }
   return launch_ms(
       aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch,
                          kAq4Ms.depth, NR, P, EPI>,
