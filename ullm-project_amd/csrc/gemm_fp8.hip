@@ -127,12 +127,14 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
 // swizzled chunks (layout at the copy offsets below).  A lane's 32-byte MFMA
 // operand is its 16 bytes of k [0, 64) followed by those of [64, 128), for A
 // and B alike, so the k pairing matches; every LDS read is a ds_read_b128
-// without bank conflicts.  Global -> LDS moves are direct global_load_lds_dwordx4
-// (no registers); two stages alternate so the copies of step s + 1 run under
-// the MFMAs of step s.  The default 256 x 256 block (8 waves of 128 x 64)
-// measured fastest on MI355X, 1.96 PFLOP/s at M=2048, N=28672, K=4096 with
-// random operands (1.37 for a 128 x 128 block that fits two workgroups per
-// CU but doubles the operand traffic from L2).  Activation rows are copied
+// without bank conflicts.  Global -> LDS moves are direct buffer loads into
+// LDS (no registers); two stages alternate so the copies of step s + 1 run
+// under the MFMAs of step s.  The 256-row blocks (8 waves) run the
+// ping-pong main loop described at the loop; a 128 x 128 block fits two
+// workgroups per CU but doubles the operand traffic from L2 per flop (1.37
+// against 1.96 PFLOP/s for 256 x 256 before the ping-pong loop, at M=2048,
+// N=28672, K=4096), so it serves only grids the large blocks leave half
+// empty.  Activation rows are copied
 // as whole 128-byte lines (see the A stage layout below): copying them as
 // 16-row wave tiles, 64 bytes per row per copy, capped the copy pipeline at
 // 8 TB/s from L2 and the kernel at 1.75 PFLOP/s.
@@ -192,14 +194,9 @@ __device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
                                                           0, 0);
 }
 
-__device__ __forceinline__ void dma16(const void *src, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(
-      (__attribute__((address_space(1))) void *)(src),
-      (__attribute__((address_space(3))) void *)(lds_wave_base), 16, 0, 0);
-}
-
-// The same copy through a buffer resource: 32-bit lane offset, scalar
-// k-step offset, no 64-bit per-lane addresses held in registers.
+// 16 bytes per lane from a buffer resource into LDS at the wave's base
+// (M0): 32-bit lane offset, scalar k-step offset, so no 64-bit per-lane
+// addresses are held in registers.
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc,
                                           uint32_t voff, uint32_t soff,
                                           void *lds_wave_base) {
