@@ -21,7 +21,7 @@ LIB = PKG / "lib" / "libullm_hip.so"
 # Measurement aid of bench.py (a streaming-read floor kernel); not linked
 # into the product library.
 BENCH_LIB = PKG / "lib" / "libullm_bench.so"
-BENCH_SOURCES = ["bench_read.hip"]
+BENCH_SOURCES = ["bench_read.hip", "check_bf16.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["abi_v1.cpp", "linear_api.cpp", "safetensors.cpp", "evidence.hip", "noalloc.hip", "weights.hip",

@@ -29,17 +29,23 @@ __device__ __forceinline__ float bits_f32(uint32_t b) {
   return __builtin_bit_cast(float, b);
 }
 
-// bf16 <-> f32.  Decode is a shift; encode is round-to-nearest-even on the 16
-// dropped bits, with NaN kept quiet and overflow carrying into infinity.
+// bf16 <-> f32.  Decode is a shift.  Encode is round-to-nearest-even on the
+// 16 dropped bits, with NaN kept quiet (sign and upper payload kept, bit 6
+// set) and overflow carrying into infinity: gfx950's v_cvt_pk_bf16_f32, two
+// values per instruction.  That instruction equals this rule bit for bit on
+// all 2^32 inputs, denormals included (with f32 denormals enabled, as this
+// library is built); ullm_bench_bf16_convert_check re-checks it on a device.
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return bits_f32(static_cast<uint32_t>(h) << 16);
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
-  const uint32_t b = f32_bits(x);
-  if ((b & 0x7fffffffu) > 0x7f800000u) {
-    return static_cast<uint16_t>((b >> 16) | 0x0040u);
-  }
-  return static_cast<uint16_t>((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+// lo in bits 0..15, hi in bits 16..31.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
 }
 
 // f16 <-> f32 through the hardware converts (RNE, f16 denormals preserved).

@@ -266,8 +266,7 @@ __device__ __forceinline__ f32x4 quad_transpose_f32(f32x4 v, uint32_t lane) {
 }
 
 __device__ __forceinline__ u32x2 pack_bf16x4(f32x4 t) {
-  return u32x2{uint32_t(f32_to_bf16(t[0])) | (uint32_t(f32_to_bf16(t[1])) << 16),
-               uint32_t(f32_to_bf16(t[2])) | (uint32_t(f32_to_bf16(t[3])) << 16)};
+  return u32x2{f32x2_to_bf16x2(t[0], t[1]), f32x2_to_bf16x2(t[2], t[3])};
 }
 
 template <class C, uint32_t EPI>
