@@ -613,6 +613,19 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         for (int r = 0; r < 4; ++r) {
           v[r] = a.alpha * ((sm[i][r] * sn[j]) * acc[i][j][r]);
         }
+        if constexpr (!resid && !gated) {
+          // No fused epilogue: the four rows go to the chunk straight from
+          // the MFMA layout (lane: rows rq .. rq + 3 of column ncol), one
+          // 2-byte write each, instead of a lane-quad transpose.
+          const uint32_t p01 = f32x2_to_bf16x2(v[0], v[1]);
+          const uint32_t p23 = f32x2_to_bf16x2(v[2], v[3]);
+          uint16_t *c0 = chunk + rq * C::OUT_STRIDE + j * 16 + ncol;
+          c0[0] = uint16_t(p01);
+          c0[C::OUT_STRIDE] = uint16_t(p01 >> 16);
+          c0[2 * C::OUT_STRIDE] = uint16_t(p23);
+          c0[3 * C::OUT_STRIDE] = uint16_t(p23 >> 16);
+          continue;
+        }
         f32x4 t = quad_transpose_f32(v, lane);
         if constexpr (resid) {
 #pragma unroll
