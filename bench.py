@@ -164,6 +164,32 @@ def bench_gemm(r, m, n, k, steps, warmup):
             "timing": mode}
 
 
+def bench_add_quant(r, m, k, steps, warmup):
+    """The add that precedes a prefill projection fused into the per-token
+    quantization (ullm_linear_add_quantize_activations: reads a and b once,
+    writes the bf16 sum and the codes) against the two passes it replaces
+    (torch's bf16 add, then ullm_linear_quantize_activations)."""
+    torch, uh = r.torch, r.uh
+    copies = 8  # 8 x 3 x 16.8 MB at M=2048, K=4096: past the Infinity Cache
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(23)
+    ab = [(torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16),
+           torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16),
+           torch.empty((m, k), dtype=torch.bfloat16, device=r.dev)) for _ in range(copies)]
+    torch.cuda.synchronize()
+    fused = [(lambda t=t: uh.add_quantize_activations(t[0], t[1], t[2], stream=r.stream))
+             for t in ab]
+    _, us_fused, mode = r.time_sweep(fused, steps, warmup)
+
+    def two_pass(t):
+        torch.add(t[0], t[1], out=t[2])
+        uh.quantize_activations(t[2], stream=r.stream)
+
+    _, us_two, _ = r.time_sweep([(lambda t=t: two_pass(t)) for t in ab], steps, warmup)
+    return {"m": m, "k": k, "us_fused": us_fused, "us_add_then_quantize": us_two,
+            "bytes_fused": 4 * m * k + m * k + 4 * m, "timing": mode}
+
+
 def bench_vendor_gemm(r, m, n, k, steps, warmup):
     """The same FP8 GEMM through the vendor library (hipBLASLt via
     torch._scaled_mm: E4M3 x E4M3 with per-tensor scales, bf16 out), over the
@@ -372,6 +398,9 @@ def main():
         configs["fp8_gemm_m2048_k4096_n28672"] = bench_gemm(
             r, 2048, 28672, 4096, max(5, args.steps // 5), 3)
         log("gemm:", configs["fp8_gemm_m2048_k4096_n28672"])
+    if "gemm" in want:
+        configs["add_quantize_m2048_k4096"] = bench_add_quant(r, 2048, 4096, 20, 3)
+        log("add + quantize:", configs["add_quantize_m2048_k4096"])
     if "vendor_gemm" in want:
         try:
             configs["vendor_fp8_gemm_m2048_k4096_n28672"] = bench_vendor_gemm(

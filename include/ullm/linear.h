@@ -174,6 +174,27 @@ typedef struct ullm_linear_act_quant_desc_t {
   uint64_t reserved[4];
 } ullm_linear_act_quant_desc_t;
 
+/* Fused add + per-token quantization: the activations quantized are
+ * sum = bf16(a + b) (the fp32 sum of each pair of bf16 elements, rounded to
+ * nearest even), optionally also written out.  128 bytes. */
+typedef struct ullm_linear_add_act_quant_desc_t {
+  uint32_t struct_size;
+  uint32_t abi_version;
+  uint64_t m;
+  uint64_t k;
+  const void *a;           /* device bf16 [M][a_row_stride] */
+  uint64_t a_row_stride;   /* elements, 0 = K */
+  const void *b;           /* device bf16 [M][b_row_stride] */
+  uint64_t b_row_stride;   /* elements, 0 = K */
+  void *sum;               /* device bf16 [M][sum_row_stride], or null (not
+                              written); may be a or b itself, same stride */
+  uint64_t sum_row_stride; /* elements, 0 = K */
+  void *xq;                /* device u8 E4M3FN [M][K] */
+  float *x_scales;         /* device f32 [M] */
+  void *stream;
+  uint64_t reserved[4];
+} ullm_linear_add_act_quant_desc_t;
+
 typedef struct ullm_linear_weight_export_desc_t {
   uint32_t struct_size;
   uint32_t abi_version;
@@ -283,6 +304,17 @@ ULLM_HIP_API ullm_status_t ullm_linear_release_workspaces(
 /* Per-token E4M3 quantization of bf16 activations.  Stream-ordered. */
 ULLM_HIP_API ullm_status_t ullm_linear_quantize_activations(
     const ullm_linear_act_quant_desc_t *desc, ullm_error_sink_t *error_sink);
+
+/* Per-token E4M3 quantization of a + b (bf16), the add that precedes a
+ * linear layer (a residual add) fused into the quantization pass: the sum
+ * is read once, and written only when `sum` is set.  xq and x_scales equal
+ * those of ullm_linear_quantize_activations on the rounded sum.  Replaces
+ * the reference's elementwise Add (crates/ullm-core/src/op.rs:90-95: two
+ * inputs and the output of one shape and dtype) followed by the Matmul's
+ * activation quantization; the reference defines no numerics for Add.
+ * Stream-ordered. */
+ULLM_HIP_API ullm_status_t ullm_linear_add_quantize_activations(
+    const ullm_linear_add_act_quant_desc_t *desc, ullm_error_sink_t *error_sink);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
             "orc_fp8_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _F, _P, _P, ctypes.c_int]),
             "orc_aq4_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
             "orc_act_quantize": (None, [_I, _I, _P, _I, _P, _P]),
+            "orc_bf16_add": (None, [_I, _P, _P, _P]),
             "orc_fp8_gemm": (None, [_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
             "orc_silu_mul": (None, [_I, _I, _P, _P]),
             "orc_max_threads": (ctypes.c_int, []),
@@ -199,6 +200,23 @@ def act_quantize(x_bf16):
     xs = np.empty(m, np.float32)
     lib().orc_act_quantize(m, k, _p(x_bf16), k, _p(xq), _p(xs))
     return xq, xs
+
+
+def bf16_add(a_bf16, b_bf16):
+    """Elementwise bf16 add: the fp32 sum rounded to bf16 (RNE)."""
+    a = np.ascontiguousarray(a_bf16, np.uint16)
+    b = np.ascontiguousarray(b_bf16, np.uint16)
+    assert a.shape == b.shape
+    out = np.empty(a.shape, np.uint16)
+    lib().orc_bf16_add(a.size, _p(a), _p(b), _p(out))
+    return out
+
+
+def add_act_quantize(a_bf16, b_bf16):
+    """Per-token quantization of a + b: returns (codes, scales, sum)."""
+    s = bf16_add(a_bf16, b_bf16)
+    xq, xs = act_quantize(s)
+    return xq, xs, s
 
 
 def fp8_gemm(xq, xs, q, s, alpha=1.0, want64=False, threads=0):

@@ -367,6 +367,12 @@ void orc_aq4_gemv(int64_t m, int64_t n, int64_t k, const uint16_t *x,
   free(xf);
 }
 
+void orc_bf16_add(int64_t n, const uint16_t *a, const uint16_t *b, uint16_t *out) {
+  for (int64_t i = 0; i < n; ++i) {
+    out[i] = orc_bf16_from_f32(orc_bf16_to_f32(a[i]) + orc_bf16_to_f32(b[i]));
+  }
+}
+
 void orc_act_quantize(int64_t m, int64_t k, const uint16_t *x, int64_t ldx,
                       uint8_t *xq, float *xs) {
   for (int64_t i = 0; i < m; ++i) {

@@ -91,6 +91,12 @@ void orc_aq4_gemv(int64_t m, int64_t n, int64_t k, const uint16_t *x,
                   const uint16_t *zeros, float alpha, float *y32, double *y64,
                   int threads);
 
+/* Elementwise bf16 add (the Add that precedes a linear layer, whose shape
+ * contract is the reference's crates/ullm-core/src/op.rs:90-95; the reference
+ * defines no numerics for it): out = bf16(f32(a) + f32(b)), the fp32 sum
+ * rounded to nearest even.  Feeds the fused add + quantization. */
+void orc_bf16_add(int64_t n, const uint16_t *a, const uint16_t *b, uint16_t *out);
+
 /* per-token activation quantization and the FP8 x FP8 GEMM */
 void orc_act_quantize(int64_t m, int64_t k, const uint16_t *x, int64_t ldx,
                       uint8_t *xq, float *xs);

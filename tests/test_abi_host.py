@@ -65,6 +65,9 @@ int main(void) {
   F(ullm_linear_forward_desc_t, residual_dtype) F(ullm_linear_forward_desc_t, residual)
   F(ullm_linear_forward_desc_t, residual_row_stride) F(ullm_linear_forward_desc_t, reserved)
   S(ullm_linear_act_quant_desc_t) F(ullm_linear_act_quant_desc_t, xq) F(ullm_linear_act_quant_desc_t, reserved)
+  S(ullm_linear_add_act_quant_desc_t) F(ullm_linear_add_act_quant_desc_t, b)
+  F(ullm_linear_add_act_quant_desc_t, sum_row_stride) F(ullm_linear_add_act_quant_desc_t, x_scales)
+  F(ullm_linear_add_act_quant_desc_t, reserved)
   S(ullm_linear_plan_t) F(ullm_linear_plan_t, kernel) F(ullm_linear_plan_t, grid) F(ullm_linear_plan_t, split_k)
   F(ullm_linear_plan_t, reserved)
   S(ullm_linear_weight_export_desc_t) F(ullm_linear_weight_export_desc_t, values) F(ullm_linear_weight_export_desc_t, reserved)
@@ -99,6 +102,7 @@ def test_headers_compile_and_layout_matches_ctypes(uh, tmp_path):
         "ullm_linear_weight_desc_t": uh.WeightDesc, "ullm_linear_weight_info_t": uh.WeightInfo,
         "ullm_linear_forward_desc_t": uh.ForwardDesc,
         "ullm_linear_act_quant_desc_t": uh.ActQuantDesc,
+        "ullm_linear_add_act_quant_desc_t": uh.AddActQuantDesc,
         "ullm_linear_plan_t": uh.Plan,
         "ullm_linear_weight_export_desc_t": uh.ExportDesc,
         "ullm_safetensors_open_desc_t": uh.StOpenDesc,
@@ -311,6 +315,31 @@ def test_activation_quant_validation(uh):
     assert lib.ullm_linear_quantize_activations(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
     d.struct_size = 16
     assert lib.ullm_linear_quantize_activations(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
+
+
+def test_add_activation_quant_validation(uh):
+    lib = uh.lib()
+    f = lib.ullm_linear_add_quantize_activations
+    assert ctypes.sizeof(uh.AddActQuantDesc) == 128
+    d = uh.new(uh.AddActQuantDesc, m=0, k=64)
+    assert f(ctypes.byref(d), None) == uh.Status.OK
+    d = uh.new(uh.AddActQuantDesc, m=4, k=0)
+    assert f(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
+    for field in ("a_row_stride", "b_row_stride", "sum_row_stride"):
+        d = uh.new(uh.AddActQuantDesc, m=4, k=64, **{field: 32})
+        assert f(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT, field
+    d = uh.new(uh.AddActQuantDesc, m=4, k=64)  # null pointers
+    assert f(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
+    # an in-place sum with another stride than the input it replaces
+    d = uh.new(uh.AddActQuantDesc, m=4, k=64, a=0x1000, b=0x2000, sum=0x1000,
+               a_row_stride=64, sum_row_stride=128, xq=0x3000, x_scales=0x4000)
+    assert f(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
+    d = uh.new(uh.AddActQuantDesc, m=4, k=64)
+    d.reserved[2] = 1
+    assert f(ctypes.byref(d), None) == uh.Status.RESERVED_NONZERO
+    d = uh.new(uh.AddActQuantDesc, m=4, k=64)
+    d.struct_size = 16
+    assert f(ctypes.byref(d), None) == uh.Status.INVALID_ARGUMENT
 
 
 def test_python_mirror_raises_without_gpu(uh):

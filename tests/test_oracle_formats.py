@@ -127,3 +127,67 @@ def test_f16_matches_numpy(orc):
         want = x.astype(np.float16).view(np.uint16)
     assert np.array_equal(orc.f16_from_f32(x), want)
     assert np.array_equal(orc.f16_to_f32(want), want.view(np.float16).astype(np.float32))
+
+
+# ---------------------------------------------------------------- bf16 add
+
+def _bf16(values):
+    import torch
+    return torch.tensor(values, dtype=torch.float32).to(torch.bfloat16) \
+        .view(torch.int16).numpy().view(np.uint16)
+
+
+def test_bf16_add_closed_forms(orc):
+    """Ties, overflow, signed zeros and the IEEE specials of the bf16 add."""
+    one, tie, ulp = 0x3F80, 0x3B80, 0x3C00      # 1.0, 2^-8, 2^-7
+    cases = [
+        (one, tie, 0x3F80),                      # 1 + 2^-8: tie, to even (1.0)
+        (0x3F81, tie, 0x3F82),                   # (1 + 2^-7) + 2^-8: tie, to even
+        (one, ulp, 0x3F81),                      # exact
+        (0x4040, 0x4000, 0x40A0),                # 3 + 2 = 5
+        (0x7F7F, 0x7F7F, 0x7F80),                # max + max overflows to inf
+        (0xFF7F, 0xFF7F, 0xFF80),                # and to -inf
+        (0x7F80, 0xFF80, None),                  # inf + -inf: NaN
+        (0x8000, 0x8000, 0x8000),                # -0 + -0 = -0
+        (0x8000, 0x0000, 0x0000),                # -0 + +0 = +0
+        (0x4049, 0xC049, 0x0000),                # x + (-x) = +0
+        (0x0001, 0x0001, 0x0002),                # subnormals add exactly
+    ]
+    a = np.array([c[0] for c in cases], np.uint16)
+    b = np.array([c[1] for c in cases], np.uint16)
+    got = orc.bf16_add(a, b)
+    for (x, y, want), g in zip(cases, got):
+        if want is None:
+            assert (g & 0x7F80) == 0x7F80 and (g & 0x7F) != 0, (hex(x), hex(y), hex(g))
+        else:
+            assert g == want, (hex(x), hex(y), hex(g))
+    assert np.array_equal(orc.bf16_add(b, a), got)  # commutative
+
+
+def test_bf16_add_matches_torch(orc):
+    """Against torch's bfloat16 add (fp32 sum rounded to nearest even) over
+    mixed magnitudes, including sums that cancel, overflow and underflow."""
+    import torch
+    rs = np.random.default_rng(31)
+    parts = [rs.standard_normal(50000) * s for s in (1e-38, 1e-3, 1.0, 1e3, 3e38)]
+    x = np.concatenate(parts).astype(np.float32)
+    y = np.concatenate([rs.standard_normal(x.size - 20000) * 1.0,
+                        -x[:10000], x[10000:20000] * 1e-3]).astype(np.float32)
+    a, b = _bf16(x), _bf16(y)
+    ta = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    tb = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16)
+    want = (ta + tb).view(torch.int16).numpy().view(np.uint16)
+    got = orc.bf16_add(a, b)
+    nan = (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7FFF) > 0x7F80)
+
+
+def test_add_act_quantize_is_quantize_of_sum(orc):
+    rs = np.random.default_rng(32)
+    a = _bf16(rs.standard_normal((6, 300)))
+    b = _bf16(rs.standard_normal((6, 300)) * 4)
+    xq, xs, s = orc.add_act_quantize(a, b)
+    assert np.array_equal(s, orc.bf16_add(a, b))
+    q2, s2 = orc.act_quantize(s)
+    assert np.array_equal(xq, q2) and np.array_equal(xs, s2)

@@ -38,6 +38,11 @@ hipError_t launch_aq4_dequant(const uint32_t *tiles, const uint32_t *sz,
 // ------------------------------------------------------------ activations
 hipError_t launch_act_quant(const uint16_t *x, uint64_t ldx, uint64_t m,
                             uint64_t k, uint8_t *xq, float *xs, hipStream_t s);
+// Per-token quantization of x + b (bf16 sums, optionally written to `sum`).
+hipError_t launch_add_act_quant(const uint16_t *x, uint64_t ldx,
+                                const uint16_t *b, uint64_t ldb, uint16_t *sum,
+                                uint64_t lds, uint64_t m, uint64_t k,
+                                uint8_t *xq, float *xs, hipStream_t s);
 
 // ------------------------------------------------------------------ GEMV
 struct GemvArgs {

@@ -965,6 +965,55 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_quantize_activations(
   });
 }
 
+extern "C" ULLM_HIP_API ullm_status_t ullm_linear_add_quantize_activations(
+    const ullm_linear_add_act_quant_desc_t *desc, ullm_error_sink_t *error_sink) {
+  ULLM_ENTRY(error_sink, "add and quantize activations", {
+    const ullm_status_t st =
+        ullm::validate_header(desc, error_sink, "activation descriptor is null");
+    if (st != ULLM_STATUS_OK) {
+      return st;
+    }
+    if (!ullm::all_zero(desc->reserved)) {
+      return write_error(error_sink, ULLM_STATUS_RESERVED_NONZERO,
+                         "activation descriptor reserved fields must be zero");
+    }
+    if (desc->k == 0 || desc->k > kMaxDim || desc->m > kMaxDim) {
+      return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "activation dimensions out of range");
+    }
+    for (const uint64_t ld : {desc->a_row_stride, desc->b_row_stride, desc->sum_row_stride}) {
+      if (ld != 0 && ld < desc->k) {
+        return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                           "a row stride is smaller than K");
+      }
+    }
+    if (desc->m == 0) {
+      return ULLM_STATUS_OK;
+    }
+    if (desc->a == nullptr || desc->b == nullptr || desc->xq == nullptr ||
+        desc->x_scales == nullptr) {
+      return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "activation pointer is null");
+    }
+    const uint64_t lda = desc->a_row_stride ? desc->a_row_stride : desc->k;
+    const uint64_t ldb = desc->b_row_stride ? desc->b_row_stride : desc->k;
+    const uint64_t lds = desc->sum_row_stride ? desc->sum_row_stride : desc->k;
+    if (desc->sum != nullptr &&
+        ((desc->sum == desc->a && lds != lda) || (desc->sum == desc->b && lds != ldb))) {
+      return write_error(error_sink, ULLM_STATUS_INVALID_ARGUMENT,
+                         "an in-place sum needs the row stride of the input it replaces");
+    }
+    HIP_TRY(error_sink, "add and activation quantize kernel",
+            ullm::launch_add_act_quant(
+                static_cast<const uint16_t *>(desc->a), lda,
+                static_cast<const uint16_t *>(desc->b), ldb,
+                static_cast<uint16_t *>(desc->sum), lds, desc->m, desc->k,
+                static_cast<uint8_t *>(desc->xq), desc->x_scales,
+                static_cast<hipStream_t>(desc->stream)));
+    return ULLM_STATUS_OK;
+  });
+}
+
 extern "C" ULLM_HIP_API ullm_status_t ullm_linear_release_workspaces(
     int32_t device, ullm_error_sink_t *error_sink) {
   ULLM_ENTRY(error_sink, "release workspaces", {

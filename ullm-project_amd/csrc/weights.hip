@@ -221,16 +221,41 @@ __global__ __launch_bounds__(kBlock) void aq4_dequant_kernel(
 }
 
 // ------------------------------------------------------ activation quant
+// Optional fused addend: the quantized activations are x + b, each element
+// the fp32 sum of the two bf16 values rounded to bf16 (round to nearest
+// even), also written to `sum` when it is not null (`sum` may be x or b
+// itself: every element is read before the same thread writes it).
+struct AddIn {
+  const uint16_t *b = nullptr;  // null: no addend
+  uint64_t ldb = 0;
+  uint16_t *sum = nullptr;
+  uint64_t lds = 0;
+};
+
+__device__ __forceinline__ uint16_t add_bf16(uint16_t x, uint16_t y) {
+  return f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(y));
+}
+
 // One workgroup per token row: a = max|x| / 448, xq = e4m3(x / a).
+template <bool ADD>
 __global__ __launch_bounds__(kBlock) void act_quant_kernel(
-    const uint16_t *__restrict__ x, uint64_t ldx, uint64_t k,
-    uint8_t *__restrict__ xq, float *__restrict__ xs) {
+    const uint16_t *x, uint64_t ldx, uint64_t k, uint8_t *__restrict__ xq,
+    float *__restrict__ xs, AddIn add) {
   __shared__ float red[kBlock / kWave];
   const uint64_t row = blockIdx.x;
   const uint16_t *src = x + row * ldx;
+  const uint16_t *bsrc = ADD ? add.b + row * add.ldb : nullptr;
+  uint16_t *sdst = ADD && add.sum != nullptr ? add.sum + row * add.lds : nullptr;
   float amax = 0.0f;
   for (uint64_t c = threadIdx.x; c < k; c += kBlock) {
-    amax = fmaxf(amax, fabsf(bf16_to_f32(src[c])));
+    uint16_t h = src[c];
+    if constexpr (ADD) {
+      h = add_bf16(h, bsrc[c]);
+      if (sdst != nullptr) {
+        sdst[c] = h;
+      }
+    }
+    amax = fmaxf(amax, fabsf(bf16_to_f32(h)));
   }
   amax = block_max(amax, red);
   const float a = amax / 448.0f;
@@ -238,7 +263,10 @@ __global__ __launch_bounds__(kBlock) void act_quant_kernel(
     xs[row] = a;
   }
   for (uint64_t c = threadIdx.x; c < k; c += kBlock) {
-    const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(src[c]) / a);
+    // The sum written above is read back (it may have replaced x or b);
+    // without a sum output it is formed again.
+    const uint16_t h = !ADD ? src[c] : sdst != nullptr ? sdst[c] : add_bf16(src[c], bsrc[c]);
+    const uint32_t q = a == 0.0f ? 0u : f32_to_e4m3(bf16_to_f32(h) / a);
     xq[row * k + c] = static_cast<uint8_t>(q);
   }
 }
@@ -247,10 +275,10 @@ __global__ __launch_bounds__(kBlock) void act_quant_kernel(
 // multiple of 8: each thread keeps CH chunks of 8 bf16 of its row in
 // registers (one 16-byte load each), so the row is read once, and writes 8
 // codes per store.  The per-element arithmetic is that of act_quant_kernel.
-template <int CH>
+template <int CH, bool ADD>
 __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
-    const uint16_t *__restrict__ x, uint64_t ldx, uint64_t k,
-    uint8_t *__restrict__ xq, float *__restrict__ xs) {
+    const uint16_t *x, uint64_t ldx, uint64_t k, uint8_t *__restrict__ xq,
+    float *__restrict__ xs, AddIn add) {
   __shared__ float red[kBlock / kWave];
   const uint64_t row = blockIdx.x;
   const uint16_t *src = x + row * ldx;
@@ -263,6 +291,22 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
     const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
     v[c] = idx < k ? *reinterpret_cast<const u32x4 *>(src + idx)
                    : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (ADD) {
+      if (idx < k) {
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(add.b + row * add.ldb + idx);
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          r[e] = f32x2_to_bf16x2(bits_f32(v[c][e] << 16) + bits_f32(b[e] << 16),
+                                 bits_f32(v[c][e] & 0xffff0000u) +
+                                     bits_f32(b[e] & 0xffff0000u));
+        }
+        v[c] = r;
+        if (add.sum != nullptr) {
+          *reinterpret_cast<u32x4 *>(add.sum + row * add.lds + idx) = r;
+        }
+      }
+    }
     const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -395,22 +439,50 @@ hipError_t launch_aq4_dequant(const uint32_t *tiles, const uint32_t *sz,
   return hipGetLastError();
 }
 
-hipError_t launch_act_quant(const uint16_t *x, uint64_t ldx, uint64_t m,
-                            uint64_t k, uint8_t *xq, float *xs, hipStream_t s) {
-  const bool vec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 8 == 0 &&
-                   k % 8 == 0 && reinterpret_cast<uintptr_t>(xq) % 8 == 0;
+namespace {
+
+template <bool ADD>
+hipError_t launch_act_quant_t(const uint16_t *x, uint64_t ldx, uint64_t m,
+                              uint64_t k, uint8_t *xq, float *xs,
+                              const AddIn &add, hipStream_t s) {
+  auto a16 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  bool vec = a16(x) && ldx % 8 == 0 && k % 8 == 0 &&
+             reinterpret_cast<uintptr_t>(xq) % 8 == 0;
+  if (ADD) {
+    vec = vec && a16(add.b) && add.ldb % 8 == 0 &&
+          (add.sum == nullptr || (a16(add.sum) && add.lds % 8 == 0));
+  }
   const uint64_t chunks = (k / 8 + kBlock - 1) / kBlock;  // per thread
   if (vec && chunks <= 8) {
-    auto kernel = chunks <= 1   ? act_quant_vec_kernel<1>
-                  : chunks <= 2 ? act_quant_vec_kernel<2>
-                  : chunks <= 4 ? act_quant_vec_kernel<4>
-                                : act_quant_vec_kernel<8>;
-    hipLaunchKernelGGL(kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k, xq, xs);
+    auto kernel = chunks <= 1   ? act_quant_vec_kernel<1, ADD>
+                  : chunks <= 2 ? act_quant_vec_kernel<2, ADD>
+                  : chunks <= 4 ? act_quant_vec_kernel<4, ADD>
+                                : act_quant_vec_kernel<8, ADD>;
+    hipLaunchKernelGGL(kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k, xq, xs, add);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(act_quant_kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k,
-                     xq, xs);
+  hipLaunchKernelGGL(act_quant_kernel<ADD>, dim3(m), dim3(kBlock), 0, s, x, ldx,
+                     k, xq, xs, add);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_act_quant(const uint16_t *x, uint64_t ldx, uint64_t m,
+                            uint64_t k, uint8_t *xq, float *xs, hipStream_t s) {
+  return launch_act_quant_t<false>(x, ldx, m, k, xq, xs, AddIn{}, s);
+}
+
+hipError_t launch_add_act_quant(const uint16_t *x, uint64_t ldx,
+                                const uint16_t *b, uint64_t ldb, uint16_t *sum,
+                                uint64_t lds, uint64_t m, uint64_t k,
+                                uint8_t *xq, float *xs, hipStream_t s) {
+  AddIn add;
+  add.b = b;
+  add.ldb = ldb;
+  add.sum = sum;
+  add.lds = lds;
+  return launch_act_quant_t<true>(x, ldx, m, k, xq, xs, add, s);
 }
 
 }  // namespace ullm

@@ -159,6 +159,14 @@ class ActQuantDesc(ctypes.Structure):
                 ("x_scales", _vp), ("stream", _vp), ("reserved", _u64 * 4)]
 
 
+class AddActQuantDesc(ctypes.Structure):
+    _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("m", _u64),
+                ("k", _u64), ("a", _vp), ("a_row_stride", _u64), ("b", _vp),
+                ("b_row_stride", _u64), ("sum", _vp), ("sum_row_stride", _u64),
+                ("xq", _vp), ("x_scales", _vp), ("stream", _vp),
+                ("reserved", _u64 * 4)]
+
+
 class ExportDesc(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("memory", _u32),
                 ("reserved0", _u32), ("values", _vp), ("scales", _vp),
@@ -231,6 +239,8 @@ _SIGNATURES = {
                                    ctypes.POINTER(ErrorSink)],
     "ullm_linear_quantize_activations": [ctypes.POINTER(ActQuantDesc),
                                          ctypes.POINTER(ErrorSink)],
+    "ullm_linear_add_quantize_activations": [ctypes.POINTER(AddActQuantDesc),
+                                             ctypes.POINTER(ErrorSink)],
     "ullm_linear_forward_plan": [ctypes.POINTER(ForwardDesc), ctypes.POINTER(Plan),
                                  ctypes.POINTER(ErrorSink)],
     "ullm_linear_release_workspaces": [_i32, ctypes.POINTER(ErrorSink)],
@@ -790,6 +800,26 @@ def save_weights(path, weights, metadata=None) -> str:
     s = _Sink()
     _check(lib().ullm_linear_weights_save(ctypes.byref(d), out, s.ref), s)
     return out.raw.hex()
+
+
+def add_quantize_activations(a, b, out=None, stream=None):
+    """Per-token E4M3 quantization of a + b (bf16 [M][K] each, rounded
+    to bf16 first): returns (xq uint8 [M][K], scales f32 [M]).  ``out``
+    (bf16 [M][>=K], may be ``a`` or ``b``) receives the sum when given."""
+    import torch
+    m, k = a.shape
+    if tuple(b.shape) != (m, k) or (out is not None and tuple(out.shape) != (m, k)):
+        raise ValueError("a, b and out must have the same shape")
+    xq = torch.empty((m, k), dtype=torch.uint8, device=a.device)
+    xs = torch.empty((m,), dtype=torch.float32, device=a.device)
+    d = new(AddActQuantDesc, m=m, k=k, a=_ptr(a), a_row_stride=a.stride(0),
+            b=_ptr(b), b_row_stride=b.stride(0),
+            sum=_ptr(out) if out is not None else None,
+            sum_row_stride=out.stride(0) if out is not None else 0,
+            xq=_ptr(xq), x_scales=_ptr(xs), stream=_stream(stream))
+    s = _Sink()
+    _check(lib().ullm_linear_add_quantize_activations(ctypes.byref(d), s.ref), s)
+    return xq, xs
 
 
 def quantize_activations(x, stream=None):
