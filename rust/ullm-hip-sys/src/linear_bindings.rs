@@ -137,6 +137,26 @@ pub struct ullm_linear_act_quant_desc_t {
     pub reserved: [u64; 4],
 }
 
+/// 128 bytes.
+#[repr(C)]
+#[derive(Clone, Copy)]
+pub struct ullm_linear_add_act_quant_desc_t {
+    pub struct_size: u32,
+    pub abi_version: u32,
+    pub m: u64,
+    pub k: u64,
+    pub a: *const c_void,
+    pub a_row_stride: u64,
+    pub b: *const c_void,
+    pub b_row_stride: u64,
+    pub sum: *mut c_void,
+    pub sum_row_stride: u64,
+    pub xq: *mut c_void,
+    pub x_scales: *mut f32,
+    pub stream: *mut c_void,
+    pub reserved: [u64; 4],
+}
+
 /// 80 bytes.
 #[repr(C)]
 #[derive(Clone, Copy)]
@@ -267,6 +287,10 @@ unsafe extern "C" {
     ) -> ullm_status_t;
     pub fn ullm_linear_quantize_activations(
         desc: *const ullm_linear_act_quant_desc_t,
+        error_sink: *mut ullm_error_sink_t,
+    ) -> ullm_status_t;
+    pub fn ullm_linear_add_quantize_activations(
+        desc: *const ullm_linear_add_act_quant_desc_t,
         error_sink: *mut ullm_error_sink_t,
     ) -> ullm_status_t;
 

@@ -335,3 +335,41 @@ pub fn release_workspaces(device: i32) -> Result<(), HipError> {
     let raw = unsafe { ffi::ullm_linear_release_workspaces(device, &mut error_sink) };
     checked(raw, &buffer, error_sink.message_length)
 }
+
+/// Per-token E4M3 quantization of `a + b` (bf16 `[m][k]` each, row strides in
+/// elements, 0 = `k`), the residual add before a prefill projection fused
+/// into the quantization pass (`ullm_linear_add_quantize_activations`).
+/// `sum`, when not null, receives the bf16 sum and may be `a` or `b` itself
+/// with the same stride.  Stream-ordered; the pointers are device memory.
+#[allow(clippy::too_many_arguments)]
+pub fn add_quantize_activations(
+    m: u64,
+    k: u64,
+    a: (*const c_void, u64),
+    b: (*const c_void, u64),
+    sum: (*mut c_void, u64),
+    xq: *mut c_void,
+    x_scales: *mut f32,
+    stream: *mut c_void,
+) -> Result<(), HipError> {
+    let desc = ffi::ullm_linear_add_act_quant_desc_t {
+        struct_size: size_of::<ffi::ullm_linear_add_act_quant_desc_t>() as u32,
+        abi_version: sys::ULLM_HIP_ABI_VERSION,
+        m,
+        k,
+        a: a.0,
+        a_row_stride: a.1,
+        b: b.0,
+        b_row_stride: b.1,
+        sum: sum.0,
+        sum_row_stride: sum.1,
+        xq,
+        x_scales,
+        stream,
+        reserved: [0; 4],
+    };
+    let mut buffer = [0u8; ERROR_CAPACITY];
+    let mut error_sink = sink(&mut buffer);
+    let raw = unsafe { ffi::ullm_linear_add_quantize_activations(&desc, &mut error_sink) };
+    checked(raw, &buffer, error_sink.message_length)
+}
