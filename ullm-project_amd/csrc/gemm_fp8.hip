@@ -551,11 +551,12 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     }
   }
   if (!a.y_f32 && a.y_vec) {
-    // Per m-tile: the quad transpose turns each 16 x 16 MFMA result into
-    // one row x four columns per lane (fp32), where the fused epilogue
-    // applies (a residual read as one 4-column vector, or silu(gate) * up
-    // with the up columns from lane ^ 8), and the rounded values go to the
-    // wave's LDS chunk as 8 bytes.  The chunk's rows then leave as 16-byte
+    // Per m-tile, each 16 x 16 MFMA result goes to the wave's LDS chunk as
+    // bf16: without a fused epilogue, and for silu(gate) * up (the up
+    // columns from lane ^ 8), straight from the MFMA layout, one 2-byte
+    // write per row; with a residual, through a quad transpose to one row x
+    // four columns per lane (fp32), where the residual is read as one
+    // 4-column vector, written as 8 bytes.  The chunk's rows then leave as 16-byte
     // segments, each row of the wave's tile one contiguous run, through
     // non-temporal stores (the output is not read again by this launch, and
     // whole segments need no write combining in L2).  Measured on MI355X at
@@ -626,6 +627,28 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
           c0[3 * C::OUT_STRIDE] = uint16_t(p23 >> 16);
           continue;
         }
+        if constexpr (gated) {
+          // SiLU-gate in the MFMA layout: lane l (column ncol < 8) holds
+          // gate values whose up partners sit in lane l ^ 8 (column
+          // ncol + 8, the same rows); its four output rows go to the chunk
+          // at feature column 8 j + ncol as 2-byte writes.
+          f32x4 h;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float up = dpp_f32<kDppXor8>(v[r]);
+            h[r] = silu_f32(v[r]) * up;
+          }
+          if (ncol < 8) {
+            const uint32_t p01 = f32x2_to_bf16x2(h[0], h[1]);
+            const uint32_t p23 = f32x2_to_bf16x2(h[2], h[3]);
+            uint16_t *c0 = chunk + rq * C::OUT_STRIDE + j * 8 + ncol;
+            c0[0] = uint16_t(p01);
+            c0[C::OUT_STRIDE] = uint16_t(p01 >> 16);
+            c0[2 * C::OUT_STRIDE] = uint16_t(p23);
+            c0[3 * C::OUT_STRIDE] = uint16_t(p23 >> 16);
+          }
+          continue;
+        }
         f32x4 t = quad_transpose_f32(v, lane);
         if constexpr (resid) {
 #pragma unroll
@@ -633,21 +656,8 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
             t[e] += rv[j][e];
           }
         }
-        if constexpr (gated) {
-          f32x4 up;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            up[e] = dpp_f32<kDppXor8>(t[e]);
-            t[e] = silu_f32(t[e]) * up[e];
-          }
-          if (c4 < 8) {
-            *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 8 + c4) =
-                pack_bf16x4(t);
-          }
-        } else {
-          *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 16 + c4) =
-              pack_bf16x4(t);
-        }
+        *reinterpret_cast<u32x2 *>(chunk + row * C::OUT_STRIDE + j * 16 + c4) =
+            pack_bf16x4(t);
       }
       if (i == 0) {
         issue_next();
