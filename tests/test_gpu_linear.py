@@ -137,6 +137,8 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
 
 @pytest.mark.parametrize("m,n,k", [
     (17, 6200, 4096),    # two m-tiles, 388 stripes: register-staged, groups of 2
+    (8, 6200, 1024),     # 388 stripes, AQ4 M <= 8: single stripes, two classes
+    (4, 6200, 1024),     # the same, four classes
     (32, 16400, 1024),   # 1025 stripes: groups of 4
     (8, 65600, 1024),    # 4100 stripes: the wide configuration
     (8, 1000, 8192),     # 63 stripes, long K: single-stripe groups, 16 waves

@@ -1977,6 +1977,11 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
 //          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
 //          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
+//   medium, AQ4 M <= 8: 4 waves, single stripes (rows then packed two or
+//          four classes deep); 4096->6144 M=8 5.9 against 6.4 us, M=4 5.9
+//          against 6.4 us, 4096->8192 M=8 6.3-6.6 against 6.9 us (at M=16
+//          and 32 the groups of 2 stay ahead: 6.5 against 7.9, 8.8 against
+//          11.4 us);
 //   seven per CU (AQ4, M <= 16, exactly 7 stripes per CU): 4 waves, groups
 //          of 7, one group per CU instead of 1.75 groups of 4; AQ4
 //          4096->28672 (1792 stripes on 256 CUs) M=8 14.8-15.3 against
@@ -2006,6 +2011,7 @@ struct RsCfg {
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsSeven{4, 1, 2, 7};
+constexpr RsCfg kRsMediumPacked{4, 1, 2, 1};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
@@ -2108,7 +2114,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
   const RsCfg *c = aq4 && a.m <= 16 && stripes == 7 * cus ? &kRsSeven
                    : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
-                   : stripes >= 384  ? &kRsMedium
+                   : stripes >= 384  ? (aq4 && a.m <= 8 ? &kRsMediumPacked : &kRsMedium)
                    : a.k >= 8192     ? &kRsDeepK
                    : a.m <= 8        ? &kRsSmall
                    : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
@@ -2150,6 +2156,7 @@ hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsSeven) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSeven, P), *c, a, s);
+  if (c == &kRsMediumPacked) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMediumPacked, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
   if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
