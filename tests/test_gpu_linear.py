@@ -141,7 +141,7 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     (4, 6200, 1024),     # the same, four classes
     (32, 16400, 1024),   # 1025 stripes: groups of 4
     (8, 65600, 1024),    # 4100 stripes: the wide configuration
-    (8, 1000, 8192),     # 63 stripes, long K: single-stripe groups, 16 waves
+    (8, 1000, 8192),     # 63 stripes, long K: single stripes (16 waves AQ4, 8 FP8)
     (33, 6200, 1024),    # a second 32-row block of one row
     (4, 1000, 8192),     # AQ4 single stripes, rows packed in four classes
     (7, 1000, 8192),     # AQ4 single stripes, two classes, a ragged class

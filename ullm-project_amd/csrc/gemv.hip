@@ -1977,6 +1977,9 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
 //          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
 //          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
+//   deep K, FP8: 8 waves, single stripes, ring depth 3; FP8 M=8
+//          14336->4096 12.8 against 14.0 us (median of 5; AQ4 keeps 16
+//          waves: its M=8 measured level to slower with 8);
 //   medium, AQ4 M <= 8: 4 waves, single stripes (rows then packed two or
 //          four classes deep); 4096->6144 M=8 5.9 against 6.4 us, M=4 5.9
 //          against 6.4 us, 4096->8192 M=8 6.3-6.6 against 6.9 us (at M=16
@@ -2010,8 +2013,12 @@ struct RsCfg {
 #endif
 constexpr RsCfg kRsWide{ULLM_RS_WIDE};
 constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
-constexpr RsCfg kRsSeven{4, 1, 2, 7};
+#ifndef ULLM_RS_SEVEN
+#define ULLM_RS_SEVEN 4, 1, 2, 7
+#endif
+constexpr RsCfg kRsSeven{ULLM_RS_SEVEN};
 constexpr RsCfg kRsMediumPacked{4, 1, 2, 1};
+constexpr RsCfg kRsDeepKFp8{8, 1, 3, 1};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
@@ -2115,7 +2122,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
                    : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
                    : stripes >= 384  ? (aq4 && a.m <= 8 ? &kRsMediumPacked : &kRsMedium)
-                   : a.k >= 8192     ? &kRsDeepK
+                   : a.k >= 8192     ? (aq4 ? &kRsDeepK : &kRsDeepKFp8)
                    : a.m <= 8        ? &kRsSmall
                    : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
                                      : nullptr;
@@ -2147,6 +2154,7 @@ hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
+  if (c == &kRsDeepKFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepKFp8, P), *c, a, s);
   if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
   return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
