@@ -1977,6 +1977,10 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
 //          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
 //          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
+//   FP8 medium and small, wide rows: 8 waves (groups of 2 and single
+//          stripes); M=32 4096->6144 10.4 against 10.8 us, 4096->4096 M=24
+//          8.6 against 9.5, M=32 9.2 against 9.6 us (AQ4 keeps 4 waves: its
+//          M=32 measured 9.3 against 8.8 and 7.6 against 7.1 us with 8);
 //   deep K, FP8: 8 waves, single stripes, ring depth 3; FP8 M=8
 //          14336->4096 12.8 against 14.0 us (median of 5; AQ4 keeps 16
 //          waves: its M=8 measured level to slower with 8);
@@ -2019,6 +2023,8 @@ constexpr RsCfg kRsLarge{ULLM_RS_LARGE};
 constexpr RsCfg kRsSeven{ULLM_RS_SEVEN};
 constexpr RsCfg kRsMediumPacked{4, 1, 2, 1};
 constexpr RsCfg kRsDeepKFp8{8, 1, 3, 1};
+constexpr RsCfg kRsMediumFp8{8, 1, 2, 2};
+constexpr RsCfg kRsSmallWideFp8{8, 1, 2, 1};
 constexpr RsCfg kRsMedium{ULLM_RS_MEDIUM};
 constexpr RsCfg kRsDeepK{ULLM_RS_DEEPK};
 constexpr RsCfg kRsSmall{ULLM_RS_SMALL};
@@ -2121,10 +2127,11 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
   const RsCfg *c = aq4 && a.m <= 16 && stripes == 7 * cus ? &kRsSeven
                    : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
-                   : stripes >= 384  ? (aq4 && a.m <= 8 ? &kRsMediumPacked : &kRsMedium)
+                   : stripes >= 384  ? (!aq4 ? &kRsMediumFp8
+                                        : a.m <= 8 ? &kRsMediumPacked : &kRsMedium)
                    : a.k >= 8192     ? (aq4 ? &kRsDeepK : &kRsDeepKFp8)
                    : a.m <= 8        ? &kRsSmall
-                   : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? &kRsSmallWide
+                   : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? (aq4 ? &kRsSmallWide : &kRsSmallWideFp8)
                                      : nullptr;
   if (c == nullptr && forced == 1) {
     c = &kRsMedium;
@@ -2155,6 +2162,8 @@ hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
   if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
   if (c == &kRsDeepKFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepKFp8, P), *c, a, s);
+  if (c == &kRsMediumFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMediumFp8, P), *c, a, s);
+  if (c == &kRsSmallWideFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWideFp8, P), *c, a, s);
   if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
   return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
