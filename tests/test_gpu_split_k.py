@@ -82,3 +82,25 @@ def test_split_k_with_epilogues(uh, orc, gpu):
     torch.cuda.synchronize()
     assert_close(y2.cpu().numpy(), ref_fn(xb2, *parts2)[0] + r.cpu().numpy(),
                  what="split residual")
+
+
+def test_split_k_shapes_share_workspace(uh, orc, gpu):
+    """Split launches of different stripe counts one after another through
+    the same scratch (the library's, then one caller workspace): a launch
+    with few stripes leaves partial sums where a launch with more stripes
+    keeps counters unless the counter region has one size for all, which
+    showed as wrong, run-to-run varying results of the second launch."""
+    cases = [("fp8", 17, 1000, 12288), ("aq4", 16, 4096, 14336),
+             ("fp8", 9, 300, 16384), ("aq4", 32, 4096, 14336), ("fp8", 16, 4096, 14336)]
+    setups = [(_setup(uh, orc, enc, m, n, k, tag=m + n + 7), m) for enc, m, n, k in cases]
+    refs = [ref_fn(xb, *parts)[0] for (lw, parts, ref_fn, xb), m in setups]
+    need = max(lw.workspace_size(m) for (lw, _, _, _), m in setups)
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    for workspace in (None, ws):
+        for rep in range(2):
+            for ((lw, parts, ref_fn, xb), m), ref in zip(setups, refs):
+                x = to_torch_bf16(xb, gpu)
+                y = lw.forward(x, out_dtype=torch.float32, workspace=workspace)
+                torch.cuda.synchronize()
+                assert_close(y.cpu().numpy(), ref,
+                             what=f"shared scratch {m}x{lw.n} rep {rep} ws {workspace is not None}")

@@ -2180,12 +2180,31 @@ hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
 }
 
-// Split-K configuration: groups of 4 stripes (shared activation loads), 4
-// waves, K split over ksplit workgroups per group.
-#ifndef ULLM_RS_SPLIT
-#define ULLM_RS_SPLIT 4, 1, 2, 4
-#endif
-constexpr RsCfg kRsSplit{ULLM_RS_SPLIT};
+// Split-K configurations: groups of adjacent stripes (shared activation
+// loads), K split over ksplit workgroups per group.  Measured on MI355X at
+// N = 4096, K = 14336 (medians of 3) against 4 waves in groups of 4: AQ4 in
+// groups of 2, M=16 13.3 against 15.1 us, M=32 16.4 against 21.0 us; FP8
+// with 8 waves, M=16 in groups of 2 15.9 against 17.5 us, M=24 and 32 in
+// groups of 4 19.2 against 21.9 and 20.3 against 23.5 us.
+constexpr RsCfg kRsSplitAq4{4, 1, 2, 2};
+constexpr RsCfg kRsSplitFp8Narrow{8, 1, 2, 2};  // M <= 16
+constexpr RsCfg kRsSplitFp8Wide{8, 1, 2, 4};    // 16 < M <= 32
+constexpr uint32_t kSplitMinGroup = 2;           // smallest group of the three
+
+// Counter words: one per stripe group.  The region has one size for every
+// split launch (plan_split takes fewer than 384 stripes, so at most 192
+// groups of the smallest group size): the counters of one launch then never
+// overlap the partial sums an earlier launch with fewer stripes left in the
+// same workspace, which would break the zero-on-entry invariant.
+constexpr uint32_t kSplitMaxStripes = 384;
+constexpr uint64_t kSplitCounterBytes = 1024;
+static_assert((kSplitMaxStripes + kSplitMinGroup - 1) / kSplitMinGroup * 4 <= kSplitCounterBytes,
+              "counter region holds one word per group");
+uint64_t split_cnt_bytes(const GemvArgs &) { return kSplitCounterBytes; }
+
+const RsCfg &split_cfg(const GemvArgs &a, bool aq4) {
+  return aq4 ? kRsSplitAq4 : a.m <= 16 ? kRsSplitFp8Narrow : kRsSplitFp8Wide;
+}
 
 // K parts per stripe group for this launch (1 = no split): 9 <= M <= 32
 // (one activation block), few stripes (< 384) and K >= 12288, with enough
@@ -2196,30 +2215,28 @@ constexpr RsCfg kRsSplit{ULLM_RS_SPLIT};
 // counter, partial loads: ~5 us) cost more than the split saves at M <= 8
 // (AQ4 M=8 14.3 against 11.8 us) and at K <= 8192.
 // ULLM_GEMV_SPLIT=0 disables, =N forces N parts where they divide.
-uint32_t plan_split(const GemvArgs &a, bool vec, uint32_t unit_k) {
+uint32_t plan_split(const GemvArgs &a, bool vec, bool aq4) {
   static const int forced = env_int("ULLM_GEMV_SPLIT", -1);
+  const RsCfg &c = split_cfg(a, aq4);
   const uint32_t stripes = a.n16 / 16;
-  const uint32_t k = a.units * unit_k;
-  if (forced == 0 || !vec || a.m > 32 || stripes >= 384 ||
+  const uint32_t k = a.units * (aq4 ? 128u : 64u);
+  if (forced == 0 || !vec || a.m > 32 || stripes >= kSplitMaxStripes ||
       (forced < 0 && (k < 12288 || a.m <= 8)) ||
       uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31) ||
       (uint64_t(a.m - 1) * a.ldx + a.k) * 2 >= (uint64_t(1) << 31)) {
     return 1;
   }
-  const uint32_t G = (stripes + kRsSplit.s - 1) / kRsSplit.s;
+  const uint32_t G = (stripes + c.s - 1) / c.s;
   uint32_t ks = forced > 1 ? uint32_t(forced) : (device_cu_count() + G - 1) / G;
   ks = std::min(ks, 16u);
-  const uint32_t per = uint32_t(kRsSplit.waves * kRsSplit.batch);
+  const uint32_t per = uint32_t(c.waves * c.batch);
   while (ks > 1 && a.units % (ks * per) != 0) {
     --ks;
   }
   return ks;
 }
 
-uint64_t split_cnt_bytes(const GemvArgs &a) {
-  const uint32_t G = (a.n16 / 16 + kRsSplit.s - 1) / kRsSplit.s;
-  return (uint64_t(G) * 4 + 255) / 256 * 256;
-}
+
 uint64_t split_bytes(const GemvArgs &a, uint32_t ks) {
   const uint64_t rows = a.m > 16 ? 32 : 16;
   return split_cnt_bytes(a) + uint64_t(ks) * a.n16 * rows * 4;
@@ -2227,13 +2244,15 @@ uint64_t split_bytes(const GemvArgs &a, uint32_t ks) {
 
 // One workgroup per (stripe group, K part).
 template <typename Kernel>
-hipError_t launch_split(Kernel kernel, GemvArgs a, uint32_t ks, hipStream_t s) {
-  const uint32_t groups = (a.n16 / 16 + kRsSplit.s - 1) / kRsSplit.s;
+hipError_t launch_split(Kernel kernel, const RsCfg &c, GemvArgs a, uint32_t ks,
+                        hipStream_t s) {
+  const uint32_t groups = (a.n16 / 16 + c.s - 1) / c.s;
   a.spw = 1;
   a.ksplit = ks;
-  hipLaunchKernelGGL(kernel, dim3(groups * ks), dim3(kRsSplit.waves * kWave), 0, s, a);
+  hipLaunchKernelGGL(kernel, dim3(groups * ks), dim3(c.waves * kWave), 0, s, a);
   return hipGetLastError();
 }
+#define ULLM_SPLIT_KERNEL(K, MT, C) K<MT, C.waves, C.s, C.batch, C.depth, 1, EPI, true>
 
 // Row packing of the register-staged kernels: the largest P <= the cap
 // whose classes (16 / P rows) hold M, for single-stripe groups only.  With
@@ -2327,12 +2346,12 @@ hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
   if (use_ms(a, vec, two ? 2 : 1, false)) {
     return two ? launch_fp8_ms<2, EPI>(a, s) : launch_fp8_ms<1, EPI>(a, s);
   }
-  const uint32_t ks = a.cnt != nullptr && a.m >= 8 ? plan_split(a, vec, 64) : 1;
+  const uint32_t ks = a.cnt != nullptr && a.m >= 8 ? plan_split(a, vec, false) : 1;
   if (ks > 1) {
-    return two ? launch_split(fp8_gemv_rs_kernel<2, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
-                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s)
-               : launch_split(fp8_gemv_rs_kernel<1, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
-                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s);
+    return two ? launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 2, kRsSplitFp8Wide),
+                              kRsSplitFp8Wide, a, ks, s)
+               : launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 1, kRsSplitFp8Narrow),
+                              kRsSplitFp8Narrow, a, ks, s);
   }
   // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
   if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec, false) : nullptr) {
@@ -2359,12 +2378,12 @@ template <int EPI>
 hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
-  const uint32_t ks = a.cnt != nullptr && a.m >= 4 ? plan_split(a, vec, 128) : 1;
+  const uint32_t ks = a.cnt != nullptr && a.m >= 4 ? plan_split(a, vec, true) : 1;
   if (ks > 1) {
-    return two ? launch_split(aq4_gemv_rs_kernel<2, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
-                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s)
-               : launch_split(aq4_gemv_rs_kernel<1, kRsSplit.waves, kRsSplit.s, kRsSplit.batch,
-                                                 kRsSplit.depth, 1, EPI, true>, a, ks, s);
+    return two ? launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 2, kRsSplitAq4),
+                              kRsSplitAq4, a, ks, s)
+               : launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 1, kRsSplitAq4),
+                              kRsSplitAq4, a, ks, s);
   }
   if (const RsCfg *rs = plan_rs(a, vec, true)) {
     if (two) {
@@ -2428,7 +2447,7 @@ uint32_t gemv_split_parts(const GemvArgs &a, bool aq4) {
   if (!aq4 && use_ms(a, vec, a.m > 16 ? 2 : 1, false)) {
     return 1;
   }
-  return plan_split(a, vec, aq4 ? 128 : 64);
+  return plan_split(a, vec, aq4);
 }
 
 uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4) {
