@@ -143,6 +143,8 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
     (8, 65600, 1024),    # 4100 stripes: the wide configuration
     (8, 1000, 8192),     # 63 stripes, long K: single stripes (16 waves AQ4, 8 FP8)
     (33, 6200, 1024),    # a second 32-row block of one row
+    (23, 1000, 4096),    # small grid, 16 <= M <= 32: single stripes, wide rows
+    (17, 1000, 4096),    # FP8 M = 17: the per-stripe kernel
     (4, 1000, 8192),     # AQ4 single stripes, rows packed in four classes
     (7, 1000, 8192),     # AQ4 single stripes, two classes, a ragged class
     (5, 16400, 1024),    # AQ4 groups of 4 at M = 5

@@ -1972,15 +1972,18 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          14336->4096 13.0 against 14.3 us (11.7 with rows packed);
 //   small  (< 384 stripes, M <= 8, rows packed): 8 waves, single stripes;
 //          AQ4 M=8 4096->4096 4.9 against 5.3 us;
-//   small, wide rows (< 384 stripes, AQ4 16 <= M <= 32, FP8 24 <= M <= 32):
+//   small, wide rows (< 384 stripes, AQ4 16 <= M <= 32; FP8 see below):
 //          4 waves, single stripes; 4096->4096 AQ4 M=16 6.16 against 6.35,
 //          M=32 9.66 against 10.29, FP8 M=24 8.97 against 9.34, M=32 10.16
 //          against 10.6 us (at FP8 M=17 and AQ4 M=9 the kernels used before
 //          stay ahead: 7.3 against 8.2, 5.2 against 5.6 us).
 //   FP8 medium and small, wide rows: 8 waves (groups of 2 and single
 //          stripes); M=32 4096->6144 10.4 against 10.8 us, 4096->4096 M=24
-//          8.6 against 9.5, M=32 9.2 against 9.6 us (AQ4 keeps 4 waves: its
-//          M=32 measured 9.3 against 8.8 and 7.6 against 7.1 us with 8);
+//          8.6 against 9.5, M=32 9.2 against 9.6, M=23 8.6 against 9.1
+//          and M=16 6.4 against 6.7 us (the LDS-staged kernel); at M = 17
+//          and 18 the per-stripe kernel stays ahead (7.2 against 8.4, 8.3
+//          against 8.5 us), level at M = 20 (AQ4 keeps 4 waves: its M=32
+//          measured 9.3 against 8.8 and 7.6 against 7.1 us with 8);
 //   deep K, FP8: 8 waves, single stripes, ring depth 3; FP8 M=8
 //          14336->4096 12.8 against 14.0 us (median of 5; AQ4 keeps 16
 //          waves: its M=8 measured level to slower with 8);
@@ -2064,7 +2067,10 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   if (!aq4) {
     // ... and at M < 8 on grids of at most one stripe per CU (4096 -> 4096
     // M=1: 4.79 against 5.03 us).
-    return a.m >= 8 || stripes <= device_cu_count();
+    // ... except at M >= 16 on small grids (< 384 stripes), where the
+    // register-staged single-stripe tier of 8 waves is ahead (4096 -> 4096
+    // M=16 6.46 against 6.66 us).
+    return (a.m >= 8 || stripes <= device_cu_count()) && !(a.m >= 16 && stripes < 384);
   }
   // AQ4: runs of 3+ stripes at M >= 4, taking two resident workgroups per CU
   // when the activation block leaves room for two.
@@ -2131,7 +2137,8 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
                                         : a.m <= 8 ? &kRsMediumPacked : &kRsMedium)
                    : a.k >= 8192     ? (aq4 ? &kRsDeepK : &kRsDeepKFp8)
                    : a.m <= 8        ? &kRsSmall
-                   : a.m >= (aq4 ? 16u : 24u) && a.m <= 32 ? (aq4 ? &kRsSmallWide : &kRsSmallWideFp8)
+                   : aq4 && a.m >= 16 && a.m <= 32                   ? &kRsSmallWide
+                   : !aq4 && (a.m == 16 || a.m > 20) && a.m <= 32     ? &kRsSmallWideFp8
                                      : nullptr;
   if (c == nullptr && forced == 1) {
     c = &kRsMedium;
