@@ -187,7 +187,8 @@ typedef struct ullm_linear_add_act_quant_desc_t {
   const void *b;           /* device bf16 [M][b_row_stride] */
   uint64_t b_row_stride;   /* elements, 0 = K */
   void *sum;               /* device bf16 [M][sum_row_stride], or null (not
-                              written); may be a or b itself, same stride */
+                              written); may be a or b itself, same stride;
+                              any other overlap of the buffers is undefined */
   uint64_t sum_row_stride; /* elements, 0 = K */
   void *xq;                /* device u8 E4M3FN [M][K] */
   float *x_scales;         /* device f32 [M] */
