@@ -213,6 +213,13 @@ typedef struct ullm_linear_weight_export_desc_t {
 #define ULLM_LINEAR_KERNEL_GEMM_DIRECT UINT32_C(2) /* FP8 GEMM, operands from L2 */
 #define ULLM_LINEAR_KERNEL_GEMM_LDS UINT32_C(3)    /* FP8 GEMM, LDS-pipelined */
 
+/* GEMV kernel variants reported by ullm_linear_forward_plan. */
+#define ULLM_LINEAR_GEMV_SINGLE UINT32_C(1)  /* one stripe per workgroup, x from L2 */
+#define ULLM_LINEAR_GEMV_SINGLE_LDS UINT32_C(2) /* one stripe per workgroup, x in LDS */
+#define ULLM_LINEAR_GEMV_MULTI_STRIPE UINT32_C(3) /* x in LDS, a run of stripes */
+#define ULLM_LINEAR_GEMV_REGISTER_STAGED UINT32_C(4) /* x in registers, stripe groups */
+#define ULLM_LINEAR_GEMV_SPLIT_K UINT32_C(5) /* register-staged, K split over workgroups */
+
 /* The launch a forward call with a given descriptor makes (diagnostics: the
  * parity tests use it to prove which kernel configuration they cover). */
 typedef struct ullm_linear_plan_t {
@@ -224,7 +231,11 @@ typedef struct ullm_linear_plan_t {
   uint32_t tiles;   /* GEMM: output tiles */
   uint32_t grid;    /* GEMM: workgroups; grid < tiles = persistent grid */
   uint32_t split_k; /* GEMV: K parts per stripe group (1 = no split) */
-  uint64_t reserved[4];
+  uint32_t gemv_variant; /* GEMV: ULLM_LINEAR_GEMV_* (0 otherwise) */
+  uint32_t gemv_waves;   /* GEMV: waves per workgroup */
+  uint32_t gemv_stripes; /* GEMV: stripes sharing one activation load */
+  uint32_t gemv_row_classes; /* GEMV: activation row classes per MFMA (1 = none) */
+  uint64_t reserved[2];
 } ullm_linear_plan_t;
 
 #ifdef __cplusplus

@@ -36,6 +36,11 @@ pub const ULLM_LINEAR_ACT_FP8_PER_TOKEN: u32 = 1;
 pub const ULLM_LINEAR_KERNEL_GEMV: u32 = 1;
 pub const ULLM_LINEAR_KERNEL_GEMM_DIRECT: u32 = 2;
 pub const ULLM_LINEAR_KERNEL_GEMM_LDS: u32 = 3;
+pub const ULLM_LINEAR_GEMV_SINGLE: u32 = 1;
+pub const ULLM_LINEAR_GEMV_SINGLE_LDS: u32 = 2;
+pub const ULLM_LINEAR_GEMV_MULTI_STRIPE: u32 = 3;
+pub const ULLM_LINEAR_GEMV_REGISTER_STAGED: u32 = 4;
+pub const ULLM_LINEAR_GEMV_SPLIT_K: u32 = 5;
 
 #[repr(C)]
 pub struct ullm_linear_weight_t {
@@ -118,7 +123,11 @@ pub struct ullm_linear_plan_t {
     pub tiles: u32,
     pub grid: u32,
     pub split_k: u32,
-    pub reserved: [u64; 4],
+    pub gemv_variant: u32,
+    pub gemv_waves: u32,
+    pub gemv_stripes: u32,
+    pub gemv_row_classes: u32,
+    pub reserved: [u64; 2],
 }
 
 /// 96 bytes.

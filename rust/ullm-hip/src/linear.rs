@@ -246,7 +246,11 @@ impl LinearWeight {
             tiles: 0,
             grid: 0,
             split_k: 0,
-            reserved: [0; 4],
+            gemv_variant: 0,
+            gemv_waves: 0,
+            gemv_stripes: 0,
+            gemv_row_classes: 0,
+            reserved: [0; 2],
         };
         let mut buffer = [0u8; ERROR_CAPACITY];
         let mut error_sink = sink(&mut buffer);

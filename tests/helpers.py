@@ -53,3 +53,20 @@ def assert_close(y, y_ref, bf16_out=False, rel=REL_TOL, what=""):
         f"{what}: max|d|={float(err.max()):.3e} rms={rms:.3e} "
         f"outliers={int(np.sum(err > bound))}")
     return float(err.max()) / rms if rms else 0.0
+
+
+GEMV_VARIANTS = {1: "single", 2: "single_lds", 3: "multi", 4: "rs", 5: "split"}
+
+
+def check_gemv_plan(lw, x, y, expect):
+    """The decode launch ullm_linear_forward_plan reports for (x, y) is
+    `expect` = (variant, waves, stripes per group, row classes).  The
+    expectations were read on a 256-CU MI355X; the launcher's grid tiers
+    depend on the CU count, so other devices skip the check."""
+    import torch
+    if torch.cuda.get_device_properties(x.device).multi_processor_count != 256:
+        return
+    p = lw.plan(x, y)
+    got = (GEMV_VARIANTS.get(p.gemv_variant, p.gemv_variant), p.gemv_waves,
+           p.gemv_stripes, p.gemv_row_classes)
+    assert got == tuple(expect), f"plan {got}, expected {tuple(expect)}"

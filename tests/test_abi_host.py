@@ -69,6 +69,7 @@ int main(void) {
   F(ullm_linear_add_act_quant_desc_t, sum_row_stride) F(ullm_linear_add_act_quant_desc_t, x_scales)
   F(ullm_linear_add_act_quant_desc_t, reserved)
   S(ullm_linear_plan_t) F(ullm_linear_plan_t, kernel) F(ullm_linear_plan_t, grid) F(ullm_linear_plan_t, split_k)
+  F(ullm_linear_plan_t, gemv_variant) F(ullm_linear_plan_t, gemv_row_classes)
   F(ullm_linear_plan_t, reserved)
   S(ullm_linear_weight_export_desc_t) F(ullm_linear_weight_export_desc_t, values) F(ullm_linear_weight_export_desc_t, reserved)
   S(ullm_safetensors_open_desc_t) F(ullm_safetensors_open_desc_t, expected_sha256) F(ullm_safetensors_open_desc_t, reserved)
@@ -82,6 +83,16 @@ int main(void) {
   return 0;
 }
 """
+
+
+def test_python_constants_mirror_header_macros(uh):
+    """Every ULLM_LINEAR_* value macro of linear.h has the same value under
+    its unprefixed name in ullm_hip (the module hard-codes them)."""
+    text = (ROOT / "include" / "ullm" / "linear.h").read_text()
+    macros = re.findall(r"#define ULLM_LINEAR_(\w+) UINT32_C\((\d+)\)", text)
+    assert len(macros) >= 20
+    for name, value in macros:
+        assert getattr(uh, name) == int(value), name
 
 
 def test_headers_compile_and_layout_matches_ctypes(uh, tmp_path):

@@ -16,7 +16,8 @@ query records which kernel family served each point.
 import pytest
 import torch
 
-from helpers import activations_bf16, assert_close, bf16_tensor_to_f32, to_torch_bf16
+from helpers import (activations_bf16, assert_close, bf16_tensor_to_f32, check_gemv_plan,
+                     to_torch_bf16)
 
 pytestmark = pytest.mark.gpu
 
@@ -33,10 +34,12 @@ def _weight(uh, gpu, encoding, n, k, seed):
     return lw
 
 
-def _check(uh, orc, gpu, lw, parts, enc, m, k, tag, what):
+def _check(uh, orc, gpu, lw, parts, enc, m, k, tag, what, plan=None):
     xb = activations_bf16(orc, m, k, tag=tag)
     x = to_torch_bf16(xb, gpu)
     y = lw.forward(x)
+    if plan is not None:
+        check_gemv_plan(lw, x, y, plan)
     torch.cuda.synchronize()
     ref = (orc.fp8_gemv if enc == "fp8" else orc.aq4_gemv)(xb, *parts)[0]
     assert_close(bf16_tensor_to_f32(y), ref, bf16_out=True, what=what)
@@ -45,15 +48,17 @@ def _check(uh, orc, gpu, lw, parts, enc, m, k, tag, what):
 
 def test_config1_fp8_matvec_4096(uh, orc, gpu):
     lw = _weight(uh, gpu, uh.ENCODING_FP8_E4M3_ROW, 4096, 4096, seed=1)
+    # The multi-stripe kernel, 8 waves (the benchmarked launch).
     assert _check(uh, orc, gpu, lw, lw.export(), "fp8", 1, 4096, 11,
-                  "config #1") == uh.KERNEL_GEMV
+                  "config #1", ("multi", 8, 1, 1)) == uh.KERNEL_GEMV
     lw.destroy()
 
 
 def test_config2_aq4_matvec_14336(uh, orc, gpu):
     lw = _weight(uh, gpu, uh.ENCODING_AQ4_G128, 14336, 4096, seed=2)
+    # The multi-stripe kernel, 8 waves, rows packed in four classes.
     assert _check(uh, orc, gpu, lw, lw.export(), "aq4", 1, 4096, 12,
-                  "config #2") == uh.KERNEL_GEMV
+                  "config #2", ("multi", 8, 1, 4)) == uh.KERNEL_GEMV
     lw.destroy()
 
 

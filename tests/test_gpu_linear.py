@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from helpers import (activations_bf16, assert_close, bf16_tensor_to_f32,
-                     to_torch_bf16, weights)
+                     check_gemv_plan, to_torch_bf16, weights)
 
 pytestmark = pytest.mark.gpu
 
@@ -105,16 +105,29 @@ def test_aq4_gemv_parity(uh, orc, gpu, m, n, k):
     assert_close(bf16_tensor_to_f32(yb), y_ref, bf16_out=True, what="aq4 gemv bf16")
 
 
-@pytest.mark.parametrize("m,n", [(1, 9000), (2, 9000), (1, 25000), (2, 25000),
-                                 (2, 13000), (3, 25000), (4, 25000), (8, 12500),
-                                 (16, 12500)])
+# (variant, waves, stripes per group, row classes) on a 256-CU device.
+MANY_STRIPES_PLAN = {
+    (1, 9000): (("single_lds", 8, 1, 1), ("multi", 8, 1, 4)),
+    (2, 9000): (("single_lds", 8, 1, 1), ("multi", 8, 1, 4)),
+    (1, 25000): (("single_lds", 8, 1, 1), ("multi", 4, 1, 4)),
+    (2, 25000): (("single_lds", 8, 1, 1), ("multi", 4, 1, 4)),
+    (2, 13000): (("single_lds", 8, 1, 1), ("multi", 4, 1, 4)),
+    (3, 25000): (("single_lds", 8, 1, 1), ("multi", 8, 1, 4)),
+    (4, 25000): (("single_lds", 8, 1, 1), ("rs", 4, 4, 1)),
+    (8, 12500): (("multi", 8, 1, 1), ("rs", 4, 1, 2)),
+    (16, 12500): (("multi", 8, 1, 1), ("rs", 4, 2, 1)),
+}
+
+
+@pytest.mark.parametrize("m,n", list(MANY_STRIPES_PLAN))
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
-    """Enough 16-row stripes (the last one ragged) that the launcher gives each
-    workgroup of the multi-stripe kernels a run of three or more stripes (at
-    M >= 4, on a 256-CU device; AQ4 M = 1 at 1563 stripes and M = 2 at 813
-    or more take the whole-stripes-per-wave configuration); K = 4096 as in
-    the Llama shapes."""
+    """Grids of 563 to 1563 16-row stripes (the last one ragged), K = 4096 as
+    in the Llama shapes: more stripes than CUs.  On a 256-CU device AQ4
+    M <= 3 takes the multi-stripe kernel (one stripe per wave at M = 1 from
+    1536 stripes and at M = 2 from 768), AQ4 M >= 4 the register-staged
+    kernel, FP8 M >= 8 the multi-stripe kernel and FP8 M < 8 the
+    single-stripe LDS kernel; the test checks that plan, then the output."""
     k = 4096
     w = weights(n, k, tag=21)
     xb = activations_bf16(orc, m, k, tag=m + 200)
@@ -128,6 +141,7 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
         lw = uh.LinearWeight.from_aq4(p, s, z)
     x = to_torch_bf16(xb, gpu)
     y32 = lw.forward(x, out_dtype=torch.float32)
+    check_gemv_plan(lw, x, y32, MANY_STRIPES_PLAN[(m, n)][enc == "aq4"])
     torch.cuda.synchronize()
     assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} gemv f32 many stripes")
     yb = lw.forward(x)
@@ -135,31 +149,54 @@ def test_gemv_parity_many_stripes(uh, orc, gpu, enc, m, n):
                  what=f"{enc} gemv bf16 many stripes")
 
 
-@pytest.mark.parametrize("m,n,k", [
-    (17, 6200, 4096),    # two m-tiles, 388 stripes: register-staged, groups of 2
-    (8, 6200, 1024),     # 388 stripes, AQ4 M <= 8: single stripes, two classes
-    (4, 6200, 1024),     # the same, four classes
-    (32, 16400, 1024),   # 1025 stripes: groups of 4
-    (8, 65600, 1024),    # 4100 stripes: the wide configuration
-    (8, 1000, 8192),     # 63 stripes, long K: single stripes (16 waves AQ4, 8 FP8)
-    (33, 6200, 1024),    # a second 32-row block of one row
-    (23, 1000, 4096),    # small grid, 16 <= M <= 32: single stripes, wide rows
-    (17, 1000, 4096),    # FP8 M = 17: the per-stripe kernel
-    (4, 1000, 8192),     # AQ4 single stripes, rows packed in four classes
-    (7, 1000, 8192),     # AQ4 single stripes, two classes, a ragged class
-    (5, 16400, 1024),    # AQ4 groups of 4 at M = 5
-    (6, 65600, 1024),    # AQ4 wide configuration at M = 6
-    (8, 1000, 4096),     # AQ4 small grid: single stripes, 8 waves, packed
-    (5, 300, 2048),      # AQ4 small grid, ragged last stripe
-    (8, 28672, 1024),    # 1792 stripes: AQ4 groups of 7 (7 per CU on 256 CUs)
-    (13, 28672, 1024),   # the same with a ragged 16-row tile
-])
+# Shapes that select each tier, and the plan on a 256-CU device:
+# (m, n, k): (FP8 plan, AQ4 plan), plan = (variant, waves, stripes, classes).
+TIER_PLAN = {
+    # two m-tiles, 388 stripes: register-staged, groups of 2
+    (17, 6200, 4096): (("rs", 8, 2, 1), ("rs", 4, 2, 1)),
+    # 388 stripes, AQ4 M <= 8: single stripes, two classes
+    (8, 6200, 1024): (("rs", 8, 2, 1), ("rs", 4, 1, 2)),
+    # the same, four classes (FP8: its activation block fits LDS)
+    (4, 6200, 1024): (("single_lds", 8, 1, 1), ("rs", 4, 1, 4)),
+    # 1025 stripes: groups of 4
+    (32, 16400, 1024): (("rs", 4, 4, 1), ("rs", 4, 4, 1)),
+    # 4100 stripes: the wide configuration
+    (8, 65600, 1024): (("rs", 8, 4, 1), ("rs", 8, 4, 1)),
+    # 63 stripes, long K: single stripes (16 waves AQ4, 8 FP8)
+    (8, 1000, 8192): (("rs", 8, 1, 2), ("rs", 16, 1, 2)),
+    # a second 32-row block of one row
+    (33, 6200, 1024): (("rs", 8, 2, 1), ("rs", 4, 2, 1)),
+    # small grid, 16 <= M <= 32: single stripes, wide rows
+    (23, 1000, 4096): (("rs", 8, 1, 1), ("rs", 4, 1, 1)),
+    # FP8 M = 17 on a small grid: the single-stripe LDS kernel
+    (17, 1000, 4096): (("single_lds", 8, 1, 1), ("rs", 4, 1, 1)),
+    # AQ4 single stripes, rows packed in four classes
+    (4, 1000, 8192): (("multi", 8, 1, 1), ("rs", 16, 1, 4)),
+    # AQ4 single stripes, two classes, a ragged class
+    (7, 1000, 8192): (("multi", 8, 1, 1), ("rs", 16, 1, 2)),
+    # AQ4 groups of 4 at M = 5
+    (5, 16400, 1024): (("single_lds", 8, 1, 1), ("rs", 4, 4, 1)),
+    # AQ4 wide configuration at M = 6
+    (6, 65600, 1024): (("single_lds", 8, 1, 1), ("rs", 8, 4, 1)),
+    # AQ4 small grid: single stripes, 8 waves, packed
+    (8, 1000, 4096): (("multi", 8, 1, 1), ("rs", 8, 1, 2)),
+    # AQ4 small grid, ragged last stripe
+    (5, 300, 2048): (("multi", 8, 1, 1), ("rs", 8, 1, 2)),
+    # 1792 stripes: AQ4 groups of 7 (7 per CU on 256 CUs)
+    (8, 28672, 1024): (("rs", 4, 4, 1), ("rs", 4, 7, 1)),
+    # the same with a ragged 16-row tile
+    (13, 28672, 1024): (("rs", 4, 4, 1), ("rs", 4, 7, 1)),
+}
+
+
+@pytest.mark.parametrize("m,n,k", list(TIER_PLAN))
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
     """Shapes that select each grid-size tier of the register-staged
     multi-stripe kernels (M >= 8 for FP8, M >= 4 for AQ4; FP8 only where its
     activation block does not fit LDS), including the two-m-tile variant and
-    a ragged last stripe and stripe group."""
+    a ragged last stripe and stripe group; the launch plan is checked
+    against TIER_PLAN, then the output against the oracle."""
     w = weights(n, k, tag=31)
     xb = activations_bf16(orc, m, k, tag=m + 300)
     if enc == "fp8":
@@ -172,6 +209,7 @@ def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
         lw = uh.LinearWeight.from_aq4(p, s, z)
     x = to_torch_bf16(xb, gpu)
     y32 = lw.forward(x, out_dtype=torch.float32)
+    check_gemv_plan(lw, x, y32, TIER_PLAN[(m, n, k)][enc == "aq4"])
     torch.cuda.synchronize()
     assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} gemv f32 {m}x{n}x{k}")
     yb = lw.forward(x)

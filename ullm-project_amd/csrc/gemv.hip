@@ -1884,10 +1884,15 @@ uint32_t lds_bytes(const GemvArgs &a, bool aq4) {
   return (rows + 1) * a.k * 2 + (aq4 ? rows * (a.k / 128) * 4 : 0);
 }
 
+// The single-stripe kernels stage the activation block in LDS when it fits.
+bool single_uses_lds(const GemvArgs &a, bool vec, bool aq4) {
+  return vec && lds_allowed() && lds_bytes(a, aq4) <= lds_cap(aq4);
+}
+
 template <int MT, int WAVES, int EPI>
 hipError_t launch_fp8_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
-  if (vec && lds_allowed() && lds_bytes(a, false) <= lds_cap(false)) {
+  if (single_uses_lds(a, vec, false)) {
     if (a.units % (WAVES * kFp8LdsBatch) == 0) {
       return launch_lds(fp8_gemv_lds_kernel<MT, WAVES, kFp8LdsBatch, true, EPI>,
                         grid, dim3(WAVES * kWave), lds_bytes(a, false), s, a);
@@ -2091,12 +2096,18 @@ hipError_t launch_ms(Kernel kernel, GemvArgs a, int waves, uint32_t lds,
   return launch_lds(kernel, grid, dim3(waves * kWave), lds, s, a);
 }
 
+// AQ4 multi-stripe launches at M <= 2 with 6 (M = 1) or 3 (M = 2) to 16
+// stripes per CU take the whole-stripe configuration.
+bool aq4_ms_whole(const GemvArgs &a) {
+  const uint32_t stripes = a.n16 / 16, cus = device_cu_count();
+  return a.m <= 2 && stripes >= (a.m == 1 ? 6 : 3) * cus && stripes < 16 * cus &&
+         a.units % uint32_t(kAq4MsWhole.batch) == 0;
+}
+
 template <int MT, int NR, int P, int EPI>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
   if constexpr (MT == 1) {
-    const uint32_t stripes = a.n16 / 16, cus = device_cu_count();
-    if (a.m <= 2 && stripes >= (a.m == 1 ? 6 : 3) * cus && stripes < 16 * cus &&
-        a.units % uint32_t(kAq4MsWhole.batch) == 0) {
+    if (aq4_ms_whole(a)) {
       constexpr MsCfg c = kAq4MsWhole;
       return launch_ms(aq4_gemv_ms_kernel<MT, c.waves, c.ks, c.batch, c.depth, NR, P, EPI>,
                        a, c.waves, ms_lds_bytes(a, true), s, c.waves / c.ks);
@@ -2283,7 +2294,7 @@ int rs_pack(const GemvArgs &a, const RsCfg *c, bool aq4) {
 template <int MT, int WAVES, int EPI>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
   const dim3 grid(a.n16 / 16, (a.m + 31) / 32);
-  if (vec && lds_allowed() && lds_bytes(a, true) <= lds_cap(true)) {
+  if (single_uses_lds(a, vec, true)) {
     if (a.units % (WAVES * kAq4LdsBatch) == 0) {
       return launch_lds(aq4_gemv_lds_kernel<MT, WAVES, kAq4LdsBatch, true, EPI>,
                         grid, dim3(WAVES * kWave), lds_bytes(a, true), s, a);
@@ -2343,33 +2354,106 @@ const char *tuning_env(const char *name) {
 #endif
 }
 
-template <int EPI>
-hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
+namespace {
+
+// The launch plan of a decode call: which kernel family, and its shape.
+// Both the launchers below and the forward plan take it from here.
+struct Choice {
+  GemvChoice info;
+  const RsCfg *rs = nullptr;  // register-staged and split-K configuration
+};
+
+Choice choose_fp8(const GemvArgs &a, bool split_ok) {
+  Choice c;
   const bool vec = x_vec_ok(a, 64);
   const bool two = a.m > 16;
   // FP8 keeps the LDS-staged kernel where the activation block fits (M=8
   // 4096->28672: 21.0 against 25.3 us register-staged); AQ4, whose per-byte
   // work is heavier, gains from the register-staged kernel there too.
   if (use_ms(a, vec, two ? 2 : 1, false)) {
-    return two ? launch_fp8_ms<2, EPI>(a, s) : launch_fp8_ms<1, EPI>(a, s);
+    c.info.variant = ULLM_LINEAR_GEMV_MULTI_STRIPE;
+    c.info.waves = kFp8Ms.waves;
+    return c;
   }
-  const uint32_t ks = a.cnt != nullptr && a.m >= 8 ? plan_split(a, vec, false) : 1;
+  const uint32_t ks = split_ok && a.m >= 8 ? plan_split(a, vec, false) : 1;
   if (ks > 1) {
-    return two ? launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 2, kRsSplitFp8Wide),
-                              kRsSplitFp8Wide, a, ks, s)
-               : launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 1, kRsSplitFp8Narrow),
-                              kRsSplitFp8Narrow, a, ks, s);
+    c.rs = two ? &kRsSplitFp8Wide : &kRsSplitFp8Narrow;
+    c.info.variant = ULLM_LINEAR_GEMV_SPLIT_K;
+    c.info.ks = ks;
+  } else if ((c.rs = a.m >= 8 ? plan_rs(a, vec, false) : nullptr)) {
+    // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
+    c.info.variant = ULLM_LINEAR_GEMV_REGISTER_STAGED;
+    c.info.classes = two ? 1 : uint32_t(rs_pack(a, c.rs, false) == 2 ? 2 : 1);
   }
-  // At M < 8 the single-stripe LDS kernel below stays ahead for FP8.
-  if (const RsCfg *rs = a.m >= 8 ? plan_rs(a, vec, false) : nullptr) {
-    if (two) {
-      return launch_fp8_rs<2, 1, EPI>(a, rs, s);
-    }
-    return rs_pack(a, rs, false) == 2 ? launch_fp8_rs<1, 2, EPI>(a, rs, s)
-                                  : launch_fp8_rs<1, 1, EPI>(a, rs, s);
+  if (c.rs != nullptr) {
+    c.info.waves = c.rs->waves;
+    c.info.stripes = c.rs->s;
+    return c;
   }
-  const int waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
-  switch (waves * 2 + (two ? 1 : 0)) {
+  c.info.variant = single_uses_lds(a, vec, false) ? ULLM_LINEAR_GEMV_SINGLE_LDS
+                                                  : ULLM_LINEAR_GEMV_SINGLE;
+  c.info.waves = pick_waves(false, a.n16 / 16, (a.m + 31) / 32, a.units);
+  return c;
+}
+
+Choice choose_aq4(const GemvArgs &a, bool split_ok) {
+  Choice c;
+  const bool vec = x_vec_ok(a, 128);
+  const bool two = a.m > 16;
+  const uint32_t ks = split_ok && a.m >= 4 ? plan_split(a, vec, true) : 1;
+  if (ks > 1) {
+    c.rs = &kRsSplitAq4;
+    c.info.variant = ULLM_LINEAR_GEMV_SPLIT_K;
+    c.info.ks = ks;
+  } else if ((c.rs = plan_rs(a, vec, true))) {
+    c.info.variant = ULLM_LINEAR_GEMV_REGISTER_STAGED;
+    c.info.classes = two ? 1 : uint32_t(rs_pack(a, c.rs, true));
+  }
+  if (c.rs != nullptr) {
+    c.info.waves = c.rs->waves;
+    c.info.stripes = c.rs->s;
+    return c;
+  }
+  if (use_ms(a, vec, two ? 2 : 1, true)) {
+    // Rows packed four classes deep up to M = 4 (ULLM_GEMV_PACK < 4 turns
+    // this off).
+    static const int cap = env_int("ULLM_GEMV_PACK", 4);
+    c.info.variant = ULLM_LINEAR_GEMV_MULTI_STRIPE;
+    c.info.classes = !two && a.m <= 4 && cap >= 4 ? 4 : 1;
+    c.info.waves = !two && aq4_ms_whole(a) ? kAq4MsWhole.waves : kAq4Ms.waves;
+    return c;
+  }
+  c.info.variant = single_uses_lds(a, vec, true) ? ULLM_LINEAR_GEMV_SINGLE_LDS
+                                                 : ULLM_LINEAR_GEMV_SINGLE;
+  c.info.waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
+  return c;
+}
+
+}  // namespace
+
+template <int EPI>
+hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
+  const Choice c = choose_fp8(a, a.cnt != nullptr);
+  const bool vec = x_vec_ok(a, 64);
+  const bool two = a.m > 16;
+  switch (c.info.variant) {
+    case ULLM_LINEAR_GEMV_MULTI_STRIPE:
+      return two ? launch_fp8_ms<2, EPI>(a, s) : launch_fp8_ms<1, EPI>(a, s);
+    case ULLM_LINEAR_GEMV_SPLIT_K:
+      return two ? launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 2, kRsSplitFp8Wide),
+                                kRsSplitFp8Wide, a, c.info.ks, s)
+                 : launch_split(ULLM_SPLIT_KERNEL(fp8_gemv_rs_kernel, 1, kRsSplitFp8Narrow),
+                                kRsSplitFp8Narrow, a, c.info.ks, s);
+    case ULLM_LINEAR_GEMV_REGISTER_STAGED:
+      if (two) {
+        return launch_fp8_rs<2, 1, EPI>(a, c.rs, s);
+      }
+      return c.info.classes == 2 ? launch_fp8_rs<1, 2, EPI>(a, c.rs, s)
+                                 : launch_fp8_rs<1, 1, EPI>(a, c.rs, s);
+    default:
+      break;
+  }
+  switch (c.info.waves * 2 + (two ? 1 : 0)) {
     case 4: return launch_fp8_t<1, 2, EPI>(a, vec, s);
     case 5: return launch_fp8_t<2, 2, EPI>(a, vec, s);
     case 8: return launch_fp8_t<1, 4, EPI>(a, vec, s);
@@ -2383,41 +2467,38 @@ hipError_t fp8_gemv_e(const GemvArgs &a, hipStream_t s) {
 
 template <int EPI>
 hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
+  const Choice c = choose_aq4(a, a.cnt != nullptr);
   const bool vec = x_vec_ok(a, 128);
   const bool two = a.m > 16;
-  const uint32_t ks = a.cnt != nullptr && a.m >= 4 ? plan_split(a, vec, true) : 1;
-  if (ks > 1) {
-    return two ? launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 2, kRsSplitAq4),
-                              kRsSplitAq4, a, ks, s)
-               : launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 1, kRsSplitAq4),
-                              kRsSplitAq4, a, ks, s);
+  switch (c.info.variant) {
+    case ULLM_LINEAR_GEMV_SPLIT_K:
+      return two ? launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 2, kRsSplitAq4),
+                                kRsSplitAq4, a, c.info.ks, s)
+                 : launch_split(ULLM_SPLIT_KERNEL(aq4_gemv_rs_kernel, 1, kRsSplitAq4),
+                                kRsSplitAq4, a, c.info.ks, s);
+    case ULLM_LINEAR_GEMV_REGISTER_STAGED:
+      if (two) {
+        return launch_aq4_rs<2, 1, EPI>(a, c.rs, s);
+      }
+      switch (c.info.classes) {
+        case 4: return launch_aq4_rs<1, 4, EPI>(a, c.rs, s);
+        case 2: return launch_aq4_rs<1, 2, EPI>(a, c.rs, s);
+        default: return launch_aq4_rs<1, 1, EPI>(a, c.rs, s);
+      }
+    case ULLM_LINEAR_GEMV_MULTI_STRIPE:
+      if (two) {
+        return launch_aq4_ms<2, 4, 1, EPI>(a, s);
+      }
+      if (c.info.classes == 1) {
+        return launch_aq4_ms<1, 4, 1, EPI>(a, s);
+      }
+      return a.m == 1 ? launch_aq4_ms<1, 1, 4, EPI>(a, s)
+                      : a.m == 2 ? launch_aq4_ms<1, 2, 4, EPI>(a, s)
+                                 : launch_aq4_ms<1, 4, 4, EPI>(a, s);
+    default:
+      break;
   }
-  if (const RsCfg *rs = plan_rs(a, vec, true)) {
-    if (two) {
-      return launch_aq4_rs<2, 1, EPI>(a, rs, s);
-    }
-    switch (rs_pack(a, rs, true)) {
-      case 4: return launch_aq4_rs<1, 4, EPI>(a, rs, s);
-      case 2: return launch_aq4_rs<1, 2, EPI>(a, rs, s);
-      default: return launch_aq4_rs<1, 1, EPI>(a, rs, s);
-    }
-  }
-  if (use_ms(a, vec, two ? 2 : 1, true)) {
-    if (two) {
-      return launch_aq4_ms<2, 4, 1, EPI>(a, s);
-    }
-    // Rows packed four classes deep up to M = 4 (ULLM_GEMV_PACK < 4 turns
-    // this off).
-    static const int cap = env_int("ULLM_GEMV_PACK", 4);
-    if (a.m > 4 || cap < 4) {
-      return launch_aq4_ms<1, 4, 1, EPI>(a, s);
-    }
-    return a.m == 1 ? launch_aq4_ms<1, 1, 4, EPI>(a, s)
-                    : a.m == 2 ? launch_aq4_ms<1, 2, 4, EPI>(a, s)
-                               : launch_aq4_ms<1, 4, 4, EPI>(a, s);
-  }
-  const int waves = pick_waves(true, a.n16 / 16, (a.m + 31) / 32, a.units);
-  switch (waves * 2 + (two ? 1 : 0)) {
+  switch (c.info.waves * 2 + (two ? 1 : 0)) {
     case 4: return launch_aq4_t<1, 2, EPI>(a, vec, s);
     case 5: return launch_aq4_t<2, 2, EPI>(a, vec, s);
     case 8: return launch_aq4_t<1, 4, EPI>(a, vec, s);
@@ -2447,14 +2528,11 @@ hipError_t launch_aq4_gemv(const GemvArgs &a, hipStream_t s) {
 }
 
 uint32_t gemv_split_parts(const GemvArgs &a, bool aq4) {
-  if (aq4 ? a.m < 4 : a.m < 8) {
-    return 1;
-  }
-  const bool vec = x_vec_ok(a, aq4 ? 128 : 64);
-  if (!aq4 && use_ms(a, vec, a.m > 16 ? 2 : 1, false)) {
-    return 1;
-  }
-  return plan_split(a, vec, aq4);
+  return gemv_choice(a, aq4, true).ks;
+}
+
+GemvChoice gemv_choice(const GemvArgs &a, bool aq4, bool split_ok) {
+  return (aq4 ? choose_aq4(a, split_ok) : choose_fp8(a, split_ok)).info;
 }
 
 uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4) {

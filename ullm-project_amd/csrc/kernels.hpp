@@ -73,6 +73,16 @@ uint64_t gemv_scratch_bytes(const GemvArgs &a, bool aq4);
 uint32_t gemv_split_parts(const GemvArgs &a, bool aq4);
 // Offset of the partial sums inside that scratch.
 uint64_t gemv_scratch_part_offset(const GemvArgs &a);
+// Kernel family and shape a GEMV launch takes (the forward plan reports it).
+// `split_ok`: split-K scratch is available (the plan assumes it is).
+struct GemvChoice {
+  uint32_t variant = 0;  // ULLM_LINEAR_GEMV_*
+  uint32_t waves = 0;    // waves per workgroup
+  uint32_t stripes = 1;  // register-staged: stripes sharing one activation load
+  uint32_t classes = 1;  // activation row classes packed per MFMA A operand
+  uint32_t ks = 1;       // split-K: K parts per stripe group
+};
+GemvChoice gemv_choice(const GemvArgs &a, bool aq4, bool split_ok);
 
 // ------------------------------------------------------------------ GEMM
 enum GemmKind : uint32_t {

@@ -721,6 +721,8 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
     plan->kernel = 0;
     plan->block_m = plan->block_n = plan->tiles = plan->grid = 0;
     plan->split_k = 1;
+    plan->gemv_variant = plan->gemv_waves = plan->gemv_stripes = 0;
+    plan->gemv_row_classes = 0;
     if (desc->m == 0) {
       return ULLM_STATUS_OK;
     }
@@ -739,8 +741,13 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
       a.k = static_cast<uint32_t>(w->k);
       a.n16 = static_cast<uint32_t>(fp8w ? w->fp8.n16 : w->aq4.n16);
       a.units = static_cast<uint32_t>(fp8w ? w->fp8.blocks_per_stripe() : w->aq4.groups);
+      const ullm::GemvChoice c = ullm::gemv_choice(a, !fp8w, true);
       plan->kernel = ULLM_LINEAR_KERNEL_GEMV;
-      plan->split_k = ullm::gemv_split_parts(a, !fp8w);
+      plan->split_k = c.ks;
+      plan->gemv_variant = c.variant;
+      plan->gemv_waves = c.waves;
+      plan->gemv_stripes = c.stripes;
+      plan->gemv_row_classes = c.classes;
       return ULLM_STATUS_OK;
     }
     // The prefill path quantizes into a dense [M][K] workspace; pre-quantized

@@ -75,6 +75,11 @@ EPILOGUE_RESIDUAL_ADD = 2
 KERNEL_GEMV = 1
 KERNEL_GEMM_DIRECT = 2
 KERNEL_GEMM_LDS = 3
+GEMV_SINGLE = 1
+GEMV_SINGLE_LDS = 2
+GEMV_MULTI_STRIPE = 3
+GEMV_REGISTER_STAGED = 4
+GEMV_SPLIT_K = 5
 BACKEND_HIP = 1
 
 # ------------------------------------------------------------------- structs
@@ -136,7 +141,9 @@ class ForwardDesc(ctypes.Structure):
 class Plan(ctypes.Structure):
     _fields_ = [("struct_size", _u32), ("abi_version", _u32), ("kernel", _u32),
                 ("block_m", _u32), ("block_n", _u32), ("tiles", _u32),
-                ("grid", _u32), ("split_k", _u32), ("reserved", _u64 * 4)]
+                ("grid", _u32), ("split_k", _u32), ("gemv_variant", _u32),
+                ("gemv_waves", _u32), ("gemv_stripes", _u32),
+                ("gemv_row_classes", _u32), ("reserved", _u64 * 2)]
 
 
 class EvidenceRequest(ctypes.Structure):
