@@ -702,11 +702,11 @@ __device__ __forceinline__ void stage_x_pad(const GemvArgs &a, uint16_t *xs,
   }
 }
 
-// LDS bytes of the multi-stripe kernels: padded activation rows, the zero
-// row, and (AQ4) the per-(row, group) sums.
-uint32_t ms_lds_bytes(const GemvArgs &a, bool aq4) {
+// LDS bytes of the multi-stripe kernels: padded activation rows and the zero
+// row.
+uint32_t ms_lds_bytes(const GemvArgs &a) {
   const uint32_t rows = min(a.m, 32u);
-  return (rows + 1) * (a.k * 2 + 16) + (aq4 ? rows * (a.k / 128) * 4 : 0);
+  return (rows + 1) * (a.k * 2 + 16);
 }
 
 // End of one stripe for the multi-stripe kernels, for the KS waves that
@@ -778,9 +778,8 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
   }
 }
 
-// Multi-stripe AQ4 kernel.  A workgroup stages its activation block (and the
-// group sums) in LDS once and then works through a run of a.spw consecutive
-// stripes.  Its WAVES waves form WAVES / KS sub-groups; sub-group g takes
+// Multi-stripe AQ4 kernel (M <= 4).  A workgroup stages its activation block
+// in LDS once and then works through a run of a.spw consecutive stripes.  Its WAVES waves form WAVES / KS sub-groups; sub-group g takes
 // stripes g, g + WAVES / KS, ... of the run, and its KS waves split each
 // stripe's K (KS = 1: a wave owns whole stripes and needs no reduction).
 // Each wave's weight stream is one software pipeline over all its stripes: a
@@ -790,28 +789,25 @@ __device__ __forceinline__ void flush_ks(const GemvArgs &a, f32x4 (&acc)[MT],
 // or for a sub-group's missing last stripe, they read zeros from outside the
 // buffer range without touching memory), so no wait on outstanding loads is
 // forced before the data is used; the tile offset is a scalar operand of the
-// buffer load.  Staging x once per workgroup instead of once per stripe is
-// what makes LDS staging pay at M = 4..16, where x is as large as a stripe's
-// weights.
-// NR: accumulator elements that can hold a valid row (M <= 4 leaves rows
-// 4..15 of the 16-row MFMA tile empty, so only elements r < NR carry results
-// and need the per-group correction).
+// buffer load.
+// NR: accumulator elements that can hold a valid row (only rows r < NR <= M
+// carry results and need the per-group correction).
 // Requires groups % (KS * B) == 0 (every wave's share is whole batches).
 //
-// P = 4 (M <= 4): the A operand rows are packed in four classes of four, as
-// in the register-staged kernels: class c of the single A read of a group
+// The A operand rows are packed in four classes of four, as in the
+// register-staged kernels: class c of the single A read of a group
 // holds the activation rows for the group's 32-k block c, so one ones-MFMA
 // gives every class its block's activation sum and the per-(row, group) sums
 // need no separate pass over LDS (the pass and its barrier sat between the
 // arrival of x and the first MFMA: 0.8 us of the M=1 4096->14336 launch on
 // MI355X).  Block c's product is valid in class c's rows only; each lane
 // keeps its own class's, and the classes are summed at the stripe's end.
-template <int MT, int WAVES, int KS, int B, int DEPTH, int NR, int P, int EPI>
+template <int WAVES, int KS, int B, int DEPTH, int NR, int EPI>
 __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
     GemvArgs a) {
-  static_assert(NR == 4 || MT == 1, "NR < 4 only for a single m-tile");
-  static_assert(P == 1 || (P == 4 && MT == 1), "row packing: one m-tile");
+  static_assert(NR >= 1 && NR <= 4, "rows of one class");
   static_assert(WAVES % KS == 0, "sub-groups");
+  constexpr int MT = 1, P = 4;
   constexpr uint32_t SG = WAVES / KS;
   constexpr uint32_t RED = KS > 1 ? 2 * WAVES * MT * 4 * kWave : 1;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs[];
@@ -838,7 +834,6 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   const uint32_t rows = min(32u, a.m - blockIdx.y * 32);
   const uint32_t cpr = a.k / 8;
   const uint32_t pitch = cpr + 1;
-  float *gsum = reinterpret_cast<float *>(xs + (rows + 1) * pitch * 8);
 
   struct Batch {
     u32x4 w[B];
@@ -876,57 +871,22 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   }
   wait_vmcnt<(DEPTH - 1) * 2 * B>();  // this thread's activation copies landed
   lds_barrier();
-  // Group sums: 16 lanes per (row, group), one chunk each, then a butterfly.
-  for (uint32_t base = 0; P == 1 && base < rows * groups * 16;
-       base += WAVES * kWave) {
-    const uint32_t i = base + threadIdx.x;
-    const uint32_t item = i / 16, c = i % 16;
-    float sum = 0.0f;
-    if (item < rows * groups) {
-      const uint32_t r = item / groups, g = item % groups;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(
-          xs + (r * pitch + g * 16 + c) * 8);
-      sum = ((bits_f32(v.x << 16) + bits_f32(v.x & 0xffff0000u)) +
-             (bits_f32(v.y << 16) + bits_f32(v.y & 0xffff0000u))) +
-            ((bits_f32(v.z << 16) + bits_f32(v.z & 0xffff0000u)) +
-             (bits_f32(v.w << 16) + bits_f32(v.w & 0xffff0000u)));
-    }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) {
-      sum += __shfl_xor(sum, off, kWave);
-    }
-    if (item < rows * groups && c == 0) {
-      gsum[item] = sum;
-    }
-  }
-  if constexpr (P == 1) {
-    lds_barrier();
-  }
 
-  // A operand of group g, MFMA j: chunk 16 g + 4 j + lane / 16 of the lane's
-  // row, i.e. byte (16 g + 4 j) * 16 past the lane base.
-  // Packed (P = 4): lane l reads row l % 4 of class (l % 16) / 4, i.e.
-  // chunk 16 g + 4 ((l % 16) / 4) + l / 16, for the single A read of group g.
-  const char *xa[MT];
-  const float *gs[MT][4];  // group-sum row of each accumulator element
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const uint32_t m = P == 1 ? mt * 16 + lane % 16 : lane % 4;
+  // A operand of group g: lane l reads row l % 4 of class (l % 16) / 4,
+  // i.e. chunk 16 g + 4 ((l % 16) / 4) + l / 16 of that row (rows past M
+  // read the zero row).
+  const char *xa;
+  {
+    const uint32_t m = lane % 4;
     const uint32_t r = m < rows ? m : rows;
-    const uint32_t c0 = P == 1 ? 0u : 4u * ((lane % 16) / 4);
-    xa[mt] = reinterpret_cast<const char *>(xs) +
-             (r * pitch + c0 + lane / 16) * 16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t mr = mt * 16 + 4 * (lane / 16) + e;
-      gs[mt][e] = gsum + (mr < rows ? mr : 0) * groups;
-    }
+    xa = reinterpret_cast<const char *>(xs) +
+         (r * pitch + 4u * ((lane % 16) / 4) + lane / 16) * 16;
   }
   const uint32_t nmask = opaque_u32(0x000f000fu);
   const uint32_t nmagic = opaque_u32(0x43004300u);
   const bf16x8 ones = __builtin_bit_cast(
       bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-  // Class of this lane's rows (P = 4): lane / 16.
+  // Class of this lane's rows: lane / 16.
   const bool odd = (lane / 16) & 1u, high = (lane / 32) & 1u;
 
   f32x4 acc[MT];
@@ -936,12 +896,12 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
   }
   // Consume pointer: the wave's cs-th stripe, group cg.
   uint32_t cs = 0, cg = ub;
-  auto consume_packed = [&](const Batch &bt) {
+  auto consume = [&](const Batch &bt) {
     f32x4 xsum[B], p[B][4];
 #pragma unroll
     for (int i = 0; i < B; ++i) {
       const bf16x8 xa0 =
-          *reinterpret_cast<const bf16x8 *>(xa[0] + (cg + i) * 256);
+          *reinterpret_cast<const bf16x8 *>(xa + (cg + i) * 256);
       xsum[i] = mfma_bf16(xa0, ones, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -964,53 +924,10 @@ __global__ __launch_bounds__(WAVES *kWave) void aq4_gemv_ms_kernel(
         acc[0][r] += sf * (q - zoff * xsum[i][r]);
       }
     }
-  };
-  auto consume_plain = [&](const Batch &bt) {
-    f32x4 p[B][MT];
-#pragma unroll
-    for (int i = 0; i < B; ++i) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        p[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    }
-    // Independent MFMA chains interleaved (j outer, group inner).
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int i = 0; i < B; ++i) {
-        const bf16x8 bj = nib8_to_bf16_off128(bt.w[i][j], nmask, nmagic);
-        const uint32_t off = ((cg + i) * 16 + 4 * j) * 16;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          p[i][mt] = mfma_bf16(
-              *reinterpret_cast<const bf16x8 *>(xa[mt] + off), bj, p[i][mt]);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < B; ++i) {
-      const float sf = f16_to_f32(uint16_t(bt.sz[i] & 0xffffu));
-      const float zoff = 128.0f + f16_to_f32(uint16_t(bt.sz[i] >> 16));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-          acc[mt][r] += sf * (p[i][mt][r] - zoff * gs[mt][r][cg + i]);
-        }
-      }
-    }
-  };
-  auto consume = [&](const Batch &bt) {
-    if constexpr (P == 4) {
-      consume_packed(bt);
-    } else {
-      consume_plain(bt);
-    }
     cg += B;
     if (cg == ue) {  // stripe done: reduce, store, reset
       const uint32_t sr = sg + cs * SG;  // run stripe
-      flush_ks<MT, KS, P, P == 1 ? 16 : NR, EPI>(a, acc,
+      flush_ks<MT, KS, P, NR, EPI>(a, acc,
                           red + (cs & 1) * (RED / 2) + sg * KS * MT * 4 * kWave,
                           T0 + sr, 1.0f, kw, sr < nS);
 #pragma unroll
@@ -2052,7 +1969,7 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   if (!vec || !lds_allowed() || forced == 0) {
     return false;
   }
-  const uint32_t lds = ms_lds_bytes(a, aq4);
+  const uint32_t lds = ms_lds_bytes(a);
   const uint32_t stripes = a.n16 / 16;
   // Dynamic (activation block) plus static (two reduction buffers) LDS must
   // fit the CU's 160 KiB; a run's weights must stay below 2 GiB (32-bit
@@ -2060,6 +1977,12 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
   if (lds > kXLdsBytes || lds + 2u * c.waves * mt * 1024u > 160u * 1024u ||
       a.units % uint32_t(c.ks * c.batch) != 0 ||
       uint64_t(stripes) * a.units * 1024u >= (uint64_t(1) << 31)) {
+    return false;
+  }
+  // AQ4 takes this kernel only with its activation rows packed four classes
+  // deep, so at M <= 4.
+  static const int cap = env_int("ULLM_GEMV_PACK", 4);
+  if (aq4 && (a.m > 4 || cap < 4)) {
     return false;
   }
   if (forced == 1) {
@@ -2077,8 +2000,10 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
     // M=16 6.46 against 6.66 us).
     return (a.m >= 8 || stripes <= device_cu_count()) && !(a.m >= 16 && stripes < 384);
   }
-  // AQ4: runs of 3+ stripes at M >= 4, taking two resident workgroups per CU
-  // when the activation block leaves room for two.
+  // AQ4: M <= 2, or runs of 3+ stripes, taking two resident workgroups per
+  // CU when the activation block leaves room for two.  (At M = 4 the
+  // register-staged kernel, planned first, takes every launch whose
+  // activation block lies within 2 GiB.)
   const uint32_t per_cu = lds + 16u * 1024u <= 80u * 1024u ? 2u : 1u;
   return a.m <= 2 || stripes >= 3 * device_cu_count() * per_cu;
 }
@@ -2104,26 +2029,23 @@ bool aq4_ms_whole(const GemvArgs &a) {
          a.units % uint32_t(kAq4MsWhole.batch) == 0;
 }
 
-template <int MT, int NR, int P, int EPI>
+template <int NR, int EPI>
 hipError_t launch_aq4_ms(const GemvArgs &a, hipStream_t s) {
-  if constexpr (MT == 1) {
-    if (aq4_ms_whole(a)) {
-      constexpr MsCfg c = kAq4MsWhole;
-      return launch_ms(aq4_gemv_ms_kernel<MT, c.waves, c.ks, c.batch, c.depth, NR, P, EPI>,
-                       a, c.waves, ms_lds_bytes(a, true), s, c.waves / c.ks);
-    }
+  if (aq4_ms_whole(a)) {
+    constexpr MsCfg c = kAq4MsWhole;
+    return launch_ms(aq4_gemv_ms_kernel<c.waves, c.ks, c.batch, c.depth, NR, EPI>,
+                     a, c.waves, ms_lds_bytes(a), s, c.waves / c.ks);
   }
   return launch_ms(
-      aq4_gemv_ms_kernel<MT, kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch,
-                         kAq4Ms.depth, NR, P, EPI>,
-      a, kAq4Ms.waves, ms_lds_bytes(a, true), s, kAq4Ms.waves / kAq4Ms.ks);
+      aq4_gemv_ms_kernel<kAq4Ms.waves, kAq4Ms.ks, kAq4Ms.batch, kAq4Ms.depth, NR, EPI>,
+      a, kAq4Ms.waves, ms_lds_bytes(a), s, kAq4Ms.waves / kAq4Ms.ks);
 }
 
 template <int MT, int EPI>
 hipError_t launch_fp8_ms(const GemvArgs &a, hipStream_t s) {
   return launch_ms(
       fp8_gemv_ms_kernel<MT, kFp8Ms.waves, kFp8Ms.batch, kFp8Ms.depth, EPI>, a,
-      kFp8Ms.waves, ms_lds_bytes(a, false), s);
+      kFp8Ms.waves, ms_lds_bytes(a), s);
 }
 
 // Configuration of the register-staged kernel for this launch, or nullptr:
@@ -2414,13 +2336,10 @@ Choice choose_aq4(const GemvArgs &a, bool split_ok) {
     c.info.stripes = c.rs->s;
     return c;
   }
-  if (use_ms(a, vec, two ? 2 : 1, true)) {
-    // Rows packed four classes deep up to M = 4 (ULLM_GEMV_PACK < 4 turns
-    // this off).
-    static const int cap = env_int("ULLM_GEMV_PACK", 4);
+  if (use_ms(a, vec, 1, true)) {
     c.info.variant = ULLM_LINEAR_GEMV_MULTI_STRIPE;
-    c.info.classes = !two && a.m <= 4 && cap >= 4 ? 4 : 1;
-    c.info.waves = !two && aq4_ms_whole(a) ? kAq4MsWhole.waves : kAq4Ms.waves;
+    c.info.classes = 4;
+    c.info.waves = aq4_ms_whole(a) ? kAq4MsWhole.waves : kAq4Ms.waves;
     return c;
   }
   c.info.variant = single_uses_lds(a, vec, true) ? ULLM_LINEAR_GEMV_SINGLE_LDS
@@ -2485,16 +2404,10 @@ hipError_t aq4_gemv_e(const GemvArgs &a, hipStream_t s) {
         case 2: return launch_aq4_rs<1, 2, EPI>(a, c.rs, s);
         default: return launch_aq4_rs<1, 1, EPI>(a, c.rs, s);
       }
-    case ULLM_LINEAR_GEMV_MULTI_STRIPE:
-      if (two) {
-        return launch_aq4_ms<2, 4, 1, EPI>(a, s);
-      }
-      if (c.info.classes == 1) {
-        return launch_aq4_ms<1, 4, 1, EPI>(a, s);
-      }
-      return a.m == 1 ? launch_aq4_ms<1, 1, 4, EPI>(a, s)
-                      : a.m == 2 ? launch_aq4_ms<1, 2, 4, EPI>(a, s)
-                                 : launch_aq4_ms<1, 4, 4, EPI>(a, s);
+    case ULLM_LINEAR_GEMV_MULTI_STRIPE:  // M <= 4, rows packed
+      return a.m == 1 ? launch_aq4_ms<1, EPI>(a, s)
+                      : a.m == 2 ? launch_aq4_ms<2, EPI>(a, s)
+                                 : launch_aq4_ms<4, EPI>(a, s);
     default:
       break;
   }
