@@ -2095,29 +2095,47 @@ hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
 }
 
 #define ULLM_RS_KERNEL(K, MT, C, P) K<MT, C.waves, C.s, C.batch, C.depth, P, EPI, false>
+// The (configuration, m-tiles, row classes) combinations plan_rs and
+// rs_pack can select: rows are packed only in single-stripe groups, and the
+// tiers limited to M <= 16 never run two m-tiles.  Only these are compiled;
+// any other combination reports an invalid launch.
+constexpr bool rs_reachable(const RsCfg &c, int mt, int p) {
+  return (p == 1 || c.s == 1) &&
+         (mt == 1 || !(&c == &kRsSeven || &c == &kRsMediumPacked || &c == &kRsSmall));
+}
+#define ULLM_RS_CASE(K, C)                                                  \
+  if (c == &C) {                                                            \
+    if constexpr (rs_reachable(C, MT, P)) {                                 \
+      return launch_rs(ULLM_RS_KERNEL(K, MT, C, P), *c, a, s);              \
+    } else {                                                                \
+      return hipErrorInvalidValue;                                          \
+    }                                                                       \
+  }
 template <int MT, int P, int EPI>
 hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
-  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
-  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
-  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
-  if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
-  if (c == &kRsDeepKFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsDeepKFp8, P), *c, a, s);
-  if (c == &kRsMediumFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsMediumFp8, P), *c, a, s);
-  if (c == &kRsSmallWideFp8) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWideFp8, P), *c, a, s);
-  if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(fp8_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsWide)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsLarge)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsMedium)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsDeepK)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsDeepKFp8)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsMediumFp8)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsSmallWideFp8)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsSmallWide)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsSmall)
+  return hipErrorInvalidValue;
 }
 
 template <int MT, int P, int EPI>
 hipError_t launch_aq4_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
-  if (c == &kRsWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsWide, P), *c, a, s);
-  if (c == &kRsLarge) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsLarge, P), *c, a, s);
-  if (c == &kRsSeven) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSeven, P), *c, a, s);
-  if (c == &kRsMediumPacked) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMediumPacked, P), *c, a, s);
-  if (c == &kRsMedium) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsMedium, P), *c, a, s);
-  if (c == &kRsDeepK) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsDeepK, P), *c, a, s);
-  if (c == &kRsSmallWide) return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmallWide, P), *c, a, s);
-  return launch_rs(ULLM_RS_KERNEL(aq4_gemv_rs_kernel, MT, kRsSmall, P), *c, a, s);
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsWide)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsLarge)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsSeven)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsMediumPacked)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsMedium)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsDeepK)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsSmallWide)
+  ULLM_RS_CASE(aq4_gemv_rs_kernel, kRsSmall)
+  return hipErrorInvalidValue;
 }
 
 // Split-K configurations: groups of adjacent stripes (shared activation
@@ -2212,6 +2230,7 @@ int rs_pack(const GemvArgs &a, const RsCfg *c, bool aq4) {
   return cap >= 2 && a.m <= 8 ? 2 : 1;
 }
 #undef ULLM_RS_KERNEL
+#undef ULLM_RS_CASE
 
 template <int MT, int WAVES, int EPI>
 hipError_t launch_aq4_t(const GemvArgs &a, bool vec, hipStream_t s) {
