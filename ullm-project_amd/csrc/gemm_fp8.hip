@@ -170,7 +170,7 @@ struct GemmCfg {
   static constexpr uint32_t A_BYTES = A_TILES * 1024;
   static constexpr uint32_t B_BYTES = B_TILES * 1024;
   static constexpr uint32_t STAGE_BYTES = ASTAGES * A_BYTES + BSTAGES * B_BYTES;
-  // Waves issuing the global -> LDS copies (the first CW).
+  // Waves issuing each operand's global -> LDS copies (CW of them).
   static constexpr uint32_t CW = PP ? WAVES / 2 : WAVES;
   static constexpr uint32_t A_COPIES = A_TILES / CW;
   // B copies per wave; when the waves do not split B evenly, the last round
@@ -185,7 +185,15 @@ struct GemmCfg {
   // bf16 output is staged one 16-row m-tile per wave at a time, past the
   // operand stages, so the stages stay free for the next tile's copies.
   static constexpr uint32_t CHUNK_BYTES = 16 * OUT_STRIDE * 2;
-  static constexpr uint32_t LDS = STAGE_BYTES + WAVES * CHUNK_BYTES;
+  // Ping-pong with three B stages: waves 0-3 copy A one k-step ahead, waves
+  // 4-7 copy B two k-steps ahead, each in its own read phase, so the copy
+  // issue of a k-step is split over its two phases; the epilogue chunks
+  // then live in A stage 1, which the next tile's first copies leave alone.
+  static constexpr bool SPLIT = PP && BSTAGES == 3;
+  static constexpr uint32_t CHUNK_BASE = SPLIT ? A_BYTES : STAGE_BYTES;
+  static_assert(!SPLIT || (ASTAGES == 2 && WAVES * CHUNK_BYTES <= A_BYTES),
+                "epilogue chunks fit A stage 1");
+  static constexpr uint32_t LDS = SPLIT ? STAGE_BYTES : STAGE_BYTES + WAVES * CHUNK_BYTES;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
 
@@ -329,26 +337,29 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       byte_buffer(a.xq, uint32_t(uint64_t(a.m) * a.ldxq));
   const __amdgpu_buffer_rsrc_t bbuf =
       byte_buffer(a.tiles, uint32_t(uint64_t(stripes) * a.units * 1024));
-  // With the ping-pong loop only the first CW waves copy.
-  const bool copier = !C::PP || wave < C::CW;
+  // With the ping-pong loop the first CW waves copy A, and B too unless
+  // the copies are split (then the last CW waves copy B).
+  const bool a_copier = !C::PP || wave < C::CW;
+  const bool b_copier = !C::PP || (C::SPLIT ? wave >= C::CW : wave < C::CW);
+  const uint32_t cwave = wave % C::CW;
   // Copies of step ks into the given stage (default: the ring slot of ks).
   auto copy_a_to = [&](uint32_t ks, char *st) {
-    if (!copier) {
+    if (!a_copier) {
       return;
     }
 #pragma unroll
     for (uint32_t i = 0; i < C::A_COPIES; ++i) {
-      dma16_buf(abuf, aoff[i], ks * C::BK, st + (i * C::CW + wave) * 1024);
+      dma16_buf(abuf, aoff[i], ks * C::BK, st + (i * C::CW + cwave) * 1024);
     }
   };
   auto copy_b_to = [&](uint32_t ks, char *st) {
-    if (!copier) {
+    if (!b_copier) {
       return;
     }
 #pragma unroll
     for (uint32_t i = 0; i < C::B_COPIES; ++i) {
-      if (C::B_EVEN || i * C::CW + wave < C::B_TILES) {
-        dma16_buf(bbuf, boff[i], ks * 2048, st + (i * C::CW + wave) * 1024);
+      if (C::B_EVEN || i * C::CW + cwave < C::B_TILES) {
+        dma16_buf(bbuf, boff[i], ks * 2048, st + (i * C::CW + cwave) * 1024);
       }
     }
   };
@@ -400,34 +411,56 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   gemm_barrier();
 
   if constexpr (C::PP) {
-    static_assert(AAHEAD == 1 && BAHEAD == 1 && C::WAVES == 8,
-                  "ping-pong: two stages, 8 waves");
+    static_assert(AAHEAD == 1 && (BAHEAD == 1 || C::SPLIT) && C::WAVES == 8,
+                  "ping-pong: two A stages, 8 waves");
     // Waves 0-3 (group 0) and 4-7 (group 1) sit one of each per SIMD, and
     // run the same loop -- read a step's operands from LDS, barrier, run
     // its MFMAs, barrier -- with group 1 one phase behind (an extra barrier
     // before its loop, matched by one after group 0's).  While one wave of
-    // a SIMD waits on LDS the other keeps the matrix core busy.  Group 0
-    // issues all copies: those for step ks + 1 go out before it reads step
-    // ks (their stage was last read by group 1 in the phase just ended)
-    // and are waited for before the barrier that ends its MFMA phase, so
-    // they have landed before either group reads them.
+    // a SIMD waits on LDS the other keeps the matrix core busy.  With two B
+    // stages group 0 issues all copies: those for step ks + 1 go out before
+    // it reads step ks (their stage was last read by group 1 in the phase
+    // just ended) and are waited for before the barrier that ends its MFMA
+    // phase, so they have landed before either group reads them.  With
+    // three (SPLIT) group 0 issues only A that way, and group 1 issues B
+    // for step ks + 2 before it reads step ks and waits for step ks + 1's B
+    // before the barrier that ends its read phase; each phase then carries
+    // about half of a step's copy instructions.  The copies slow the loop
+    // in proportion to the instructions issued in one phase, not by their
+    // latency (waiting for them costs ~1 %): on MI355X at M=2048,
+    // N=28672 the split took a k-step of every CU's tile from 1.31 to 1.14
+    // us (K sweep 4096 -> 8192) and the launch from 207 to 197 us.
     const bool g1 = wave >= C::WAVES / 2;
     i32x8 af[C::TM], bf[C::TN];
     if (g1) {
       gemm_barrier();
     }
-    // The stage being read, kept as a counter.
-    uint32_t st = 0;
+    // The stages being read, kept as counters (A: ks % 2, B: ks % BSTAGES;
+    // bn: the B stage of step ks + 2 when B runs two steps ahead).
+    uint32_t st = 0, sb = 0, bn = 2;
     char *const bstages = lds + C::ASTAGES * C::A_BYTES;
 #pragma clang loop unroll(disable)
     for (uint32_t ks = 0; ks < ksteps; ++ks) {
-      if (ks + 1 < ksteps) {
+      if constexpr (C::SPLIT) {
+        // Group 0 copies A for step ks + 1 (its stage was last read in the
+        // phase just ended), group 1 B for step ks + 2 (its stage held
+        // step ks - 1, read by both groups before this phase).
+        if (!g1 && ks + 1 < ksteps) {
+          copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
+        }
+        if (g1 && ks + 2 < ksteps) {
+          copy_b_to(ks + 2, bstages + bn * C::B_BYTES);
+        }
+      } else if (ks + 1 < ksteps) {
         copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
         copy_b_to(ks + 1, bstages + (st ^ 1u) * C::B_BYTES);
       }
       const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
-      const char *Bs = bstages + st * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
+      const char *Bs = bstages + (C::SPLIT ? sb : st) * C::B_BYTES +
+                       (wn * C::TN * 2) * 1024 + lane * 16;
       st ^= 1u;
+      sb = sb == 2 ? 0u : sb + 1u;
+      bn = bn == 2 ? 0u : bn + 1u;
 #pragma unroll
       for (uint32_t i = 0; i < C::TM; ++i) {
         af[i] = a_operand(As, i);
@@ -435,6 +468,18 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
 #pragma unroll
       for (uint32_t j = 0; j < C::TN; ++j) {
         bf[j] = lds_operand(Bs + j * 2048);
+      }
+      if constexpr (C::SPLIT) {
+        // Group 1: step ks + 1's B copies (issued a step ago) have landed
+        // before the barrier after which group 0 reads them; step ks + 2's
+        // stay in flight.
+        if (g1) {
+          if (ks + 2 < ksteps) {
+            wait_vm<C::B_COPIES>();
+          } else {
+            __builtin_amdgcn_s_waitcnt(0);
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       gemm_barrier();
@@ -447,7 +492,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's copies have landed
+      if (!C::SPLIT || !g1) {
+        __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's A (and B) copies landed
+      }
       gemm_barrier();
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -565,7 +612,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     // stores 259-261 us, per m-tile chunk with non-temporal stores 245-247.
     constexpr bool gated = EPI == kEpiSiluMul;
     constexpr bool resid = EPI == kEpiResidual;
-    uint16_t *chunk = reinterpret_cast<uint16_t *>(lds + C::STAGE_BYTES) +
+    uint16_t *chunk = reinterpret_cast<uint16_t *>(lds + C::CHUNK_BASE) +
                       wave * (C::CHUNK_BYTES / 2);
     const uint32_t row = rq + lane % 4, c4 = (ncol / 4) * 4;
     // Gated: lanes with c4 < 8 hold gate columns, those with c4 >= 8 the
@@ -717,13 +764,18 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 // becomes a multiple of the CU count where 256-column tiles leave the last
 // round half empty.  Measured on MI355X at M=2048, N=28672: ping-pong
 // 215-220 against 232-235 us (per 128-deep k-step of every CU's tile 1.32
-// against 1.48-1.54 us, from a K sweep); a third B stage (B copies two
-// steps ahead) gained nothing.
-using GemmNarrow = GemmCfg<256, 224, 4, 2, 2, 2, true>;
+// against 1.48-1.54 us, from a K sweep).  Three B stages with the copy
+// issue split between the groups (SPLIT): 196-197 against 207 us, 1.14
+// against 1.31 us per k-step; a third B stage with group 0 still issuing
+// every copy gained nothing.
+#ifndef ULLM_GEMM_PP_BSTAGES
+#define ULLM_GEMM_PP_BSTAGES 3
+#endif
+using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_PP_BSTAGES, 2, true>;
 // 192 columns: 4 waves of 64 rows x 2 of 96 columns, ping-pong, for grids
 // where it fills the last round (M = 2048, N = 6144: 256 tiles, one full
 // round; 48.5 against 54.1 us without the ping-pong loop).
-using GemmNarrow192 = GemmCfg<256, 192, 4, 2, 2, 2, true>;
+using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_PP_BSTAGES, 2, true>;
 // 8 waves of 64 x 32; 2 workgroups per CU.  The ping-pong loop measured
 // level or slower here (two workgroups already interleave on each SIMD)
 // and needs more than the 128 registers per wave two workgroups allow.
