@@ -183,7 +183,8 @@ struct GemmCfg {
   // banks.
   static constexpr uint32_t OUT_STRIDE = TN * 16 + 8;
   // bf16 output is staged one 16-row m-tile per wave at a time, past the
-  // operand stages, so the stages stay free for the next tile's copies.
+  // operand stages (or in A stage 1, below), so the stages the next tile's
+  // first copies fill stay free.
   static constexpr uint32_t CHUNK_BYTES = 16 * OUT_STRIDE * 2;
   // Ping-pong with three B stages: waves 0-3 copy A one k-step ahead, waves
   // 4-7 copy B two k-steps ahead, each in its own read phase, so the copy
@@ -569,10 +570,11 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t cm0 = m0, cT0 = T0;
   const uint32_t next = id + gridDim.x;
   const bool more = next < total;
-  // The epilogue leaves the operand stages alone (its LDS chunk lies past
-  // them), so the next tile's first copies are issued during it: after the
-  // scales below are in use (waiting for them then does not wait for the
-  // copies) and before the stores.
+  // The epilogue leaves the stages of the next tile's first copies alone
+  // (its LDS chunks lie past the stages, or in A stage 1 with three B
+  // stages), so those copies are issued during it: after the scales below
+  // are in use (waiting for them then does not wait for the copies) and
+  // before the stores.
   auto issue_next = [&]() {
     if (more) {
       setup(next);
