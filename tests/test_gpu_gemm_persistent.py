@@ -1,4 +1,5 @@
-"""GPU parity of the prefill FP8 GEMM on its persistent multi-tile launches.
+"""GPU parity of the prefill FP8 GEMM on its persistent multi-tile launches
+and on the one-round 256 x 128 launches of the N = 4096 prefill shapes.
 
 Each shape below makes the launcher pick one block configuration with more
 output tiles than workgroups, so every workgroup walks several tiles and
@@ -25,13 +26,20 @@ from helpers import (activations_bf16, assert_close, bf16_tensor_to_f32, rng,
 
 pytestmark = pytest.mark.gpu
 
-# (configuration, M, N, K): block 256 x N_b, or "mid" = 128 x 128 two per CU.
+# (configuration, M, N, K): block 256 x N_b, or 128 x 128 two per CU.
 PERSISTENT = [
     ("256x224", 1024, 28672, 256),   # 512 tiles on 256 workgroups
     ("256x256", 200, 131072, 128),   # 512 tiles, one ragged 256-row block
     ("256x192", 250, 98304, 256),    # 512 tiles
     ("128x128", 1100, 14000, 256),   # 990 tiles on 512 workgroups, ragged N
 ]
+# One round of 256 x 128 ping-pong blocks (the N = 4096 prefill shapes): the
+# launch is not persistent, so only the block is asserted.
+ONE_ROUND = [
+    ("256x128", 2048, 4096, 256),    # 256 tiles on 256 CUs
+    ("256x128", 1024, 4000, 128),    # 128 tiles, ragged N
+]
+CASES = [c + (True,) for c in PERSISTENT] + [c + (False,) for c in ONE_ROUND]
 
 
 def _sample_rows(m, tag, per_block=6):
@@ -43,12 +51,13 @@ def _sample_rows(m, tag, per_block=6):
     return np.array(sorted(rows))
 
 
-def _plan_matches(uh, lw, x, y, cfg, **kw):
+def _plan_matches(uh, lw, x, y, cfg, persistent=True, **kw):
     p = lw.plan(x, y, mode=uh.ACT_FP8_PER_TOKEN, **kw)
     assert p.kernel == uh.KERNEL_GEMM_LDS, p.kernel
     bm, bn = (int(v) for v in cfg.split("x"))
     assert (p.block_m, p.block_n) == (bm, bn), (p.block_m, p.block_n)
-    assert p.tiles > p.grid, (p.tiles, p.grid)   # persistent: several tiles each
+    if persistent:
+        assert p.tiles > p.grid, (p.tiles, p.grid)   # several tiles each
     return p
 
 
@@ -61,8 +70,8 @@ def _fp8_weight(uh, orc, n, k, tag, gpu, gated=False):
     return lw, q, s
 
 
-@pytest.mark.parametrize("cfg,m,n,k", PERSISTENT)
-def test_persistent_gemm_no_epilogue(uh, orc, gpu, cfg, m, n, k):
+@pytest.mark.parametrize("cfg,m,n,k,persistent", CASES)
+def test_persistent_gemm_no_epilogue(uh, orc, gpu, cfg, m, n, k, persistent):
     lw, q, s = _fp8_weight(uh, orc, n, k, tag=m + n, gpu=gpu)
     xb = activations_bf16(orc, m, k, tag=m + 1)
     xq, xs = orc.act_quantize(xb)
@@ -70,7 +79,7 @@ def test_persistent_gemm_no_epilogue(uh, orc, gpu, cfg, m, n, k):
     ref = orc.fp8_gemm(xq[rows], xs[rows], q, s)[0]
     x = to_torch_bf16(xb, gpu)
     yb = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
-    _plan_matches(uh, lw, x, yb, cfg)
+    _plan_matches(uh, lw, x, yb, cfg, persistent)
     lw.forward(x, yb, mode=uh.ACT_FP8_PER_TOKEN)           # staged bf16 stores
     y32 = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN)
     torch.cuda.synchronize()
@@ -85,8 +94,8 @@ def test_persistent_gemm_no_epilogue(uh, orc, gpu, cfg, m, n, k):
                  what=f"{cfg} pre-quantized {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("cfg,m,n,k", PERSISTENT)
-def test_persistent_gemm_silu_mul(uh, orc, gpu, cfg, m, n, k):
+@pytest.mark.parametrize("cfg,m,n,k,persistent", CASES)
+def test_persistent_gemm_silu_mul(uh, orc, gpu, cfg, m, n, k, persistent):
     lw, q, s = _fp8_weight(uh, orc, n, k, tag=m + n + 1, gpu=gpu, gated=True)
     f = n // 2
     xb = activations_bf16(orc, m, k, tag=m + 2)
@@ -95,7 +104,7 @@ def test_persistent_gemm_silu_mul(uh, orc, gpu, cfg, m, n, k):
     ref = orc.silu_mul(orc.fp8_gemm(xq[rows], xs[rows], q, s)[0])
     x = to_torch_bf16(xb, gpu)
     yb = torch.empty((m, f), dtype=torch.bfloat16, device=gpu)
-    _plan_matches(uh, lw, x, yb, cfg)
+    _plan_matches(uh, lw, x, yb, cfg, persistent)
     lw.forward(x, yb, mode=uh.ACT_FP8_PER_TOKEN)
     y32 = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN)
     torch.cuda.synchronize()
@@ -104,8 +113,8 @@ def test_persistent_gemm_silu_mul(uh, orc, gpu, cfg, m, n, k):
     assert_close(y32[rows].cpu().numpy(), ref, what=f"{cfg} silu f32")
 
 
-@pytest.mark.parametrize("cfg,m,n,k", PERSISTENT)
-def test_persistent_gemm_residual(uh, orc, gpu, cfg, m, n, k):
+@pytest.mark.parametrize("cfg,m,n,k,persistent", CASES)
+def test_persistent_gemm_residual(uh, orc, gpu, cfg, m, n, k, persistent):
     lw, q, s = _fp8_weight(uh, orc, n, k, tag=m + n + 2, gpu=gpu)
     xb = activations_bf16(orc, m, k, tag=m + 3)
     rb = activations_bf16(orc, m, n, tag=m + 4)
@@ -114,7 +123,7 @@ def test_persistent_gemm_residual(uh, orc, gpu, cfg, m, n, k):
     ref = orc.fp8_gemm(xq[rows], xs[rows], q, s)[0] + orc.bf16_to_f32(rb[rows])
     x = to_torch_bf16(xb, gpu)
     y = to_torch_bf16(rb, gpu)
-    _plan_matches(uh, lw, x, y, cfg, residual=y)
+    _plan_matches(uh, lw, x, y, cfg, persistent, residual=y)
     y32 = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN,
                      residual=y.float())                    # f32 scalar epilogue
     lw.forward(x, y, residual=y, mode=uh.ACT_FP8_PER_TOKEN)  # in place, staged bf16

@@ -104,7 +104,8 @@ def test_plan_reports_launches(uh, orc, gpu):
     y = torch.empty((2048, 4096), dtype=torch.bfloat16, device=gpu)
     p = lw.plan(x, y, mode=uh.ACT_FP8_PER_TOKEN)
     assert p.kernel == uh.KERNEL_GEMM_LDS
-    assert (p.block_m, p.block_n) == (128, 128) and p.tiles == 512
+    # one round of 256 x 128 ping-pong blocks on a 256-CU device
+    assert (p.block_m, p.block_n) == (256, 128) and p.tiles == 256
     # unaligned pre-quantized activations take the direct kernel
     xq = torch.zeros((64, 4096 + 3), dtype=torch.uint8, device=gpu)[:, 3:]
     xs = torch.ones((64,), dtype=torch.float32, device=gpu)

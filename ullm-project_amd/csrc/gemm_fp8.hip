@@ -782,6 +782,10 @@ using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_PP_BSTAGES, 2, true>;
 // level or slower here (two workgroups already interleave on each SIMD)
 // and needs more than the 128 registers per wave two workgroups allow.
 using GemmMid = GemmCfg<128, 128, 2, 4>;
+// 128 columns: 4 waves of 64 rows x 2 of 64 columns, ping-pong with three B
+// stages, one workgroup per CU, for N = 4096-class grids (one full round of
+// 256 x 128 tiles at M = 2048).
+using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 2, true>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
@@ -821,6 +825,19 @@ bool gemm_use_mid(uint32_t m, uint32_t n, uint32_t cus) {
   const uint64_t tmid = uint64_t((m + 127) / 128) * ((n + 127) / 128);
   const uint64_t rounds_mid = (tmid + 2 * cus - 1) / (2 * cus);
   return double(rounds_mid) * 0.82 < double(rounds_large) * 0.95;
+}
+
+// Where the 128 x 128 blocks would win over the wide ones, 256 x 128 ping-pong
+// blocks (one workgroup per CU) win over them in turn when their grid needs
+// no more rounds and fills at least half of the CUs.  Measured on MI355X at
+// N = 4096: M=2048 K=4096 33.1 against 38.2 us, K=14336 100.6-101.2 against
+// 120.5-121.0 us, M=1024 K=4096 27.5 against 30.5 us.
+bool gemm_use_128(uint32_t m, uint32_t n, uint32_t cus) {
+  const uint64_t t128 = uint64_t((m + 255) / 256) * ((n + 127) / 128);
+  const uint64_t tmid = uint64_t((m + 127) / 128) * ((n + 127) / 128);
+  const uint64_t r128 = (t128 + cus - 1) / cus;
+  const uint64_t rmid = (tmid + 2 * cus - 1) / (2 * cus);
+  return r128 <= rmid && 2 * t128 >= cus;
 }
 
 template <class C>
@@ -884,6 +901,7 @@ hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
     case kGemmMid: return launch_gemm_lds<GemmMid, EPI>(a, p, s);
     case kGemmNarrow: return launch_gemm_lds<GemmNarrow, EPI>(a, p, s);
     case kGemmNarrow192: return launch_gemm_lds<GemmNarrow192, EPI>(a, p, s);
+    case kGemmNarrow128: return launch_gemm_lds<GemmNarrow128, EPI>(a, p, s);
     case kGemmLarge: return launch_gemm_lds<GemmLarge, EPI>(a, p, s);
     default: break;
   }
@@ -917,6 +935,13 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
   const char *persist_env = tuning_env("ULLM_GEMM_PERSIST");
   const bool persist = persist_env == nullptr || persist_env[0] != '0';
   const int forced_bn = bn_env ? std::atoi(bn_env) : 0;
+  if (forced_bn == 128 ||
+      (forced_bn == 0 && cfg == nullptr && gemm_use_mid(m, n, cus) &&
+       gemm_use_128(m, n, cus))) {
+    p.kind = kGemmNarrow128;
+    fill_plan<GemmNarrow128>(p, m, n, cus, persist);
+    return p;
+  }
   if ((cfg != nullptr && cfg[0] == 'm') ||
       (forced_bn == 0 && gemm_use_mid(m, n, cus))) {
     p.kind = kGemmMid;
