@@ -141,10 +141,6 @@ __global__ __launch_bounds__(256) void fp8_gemm_direct_kernel(GemmArgs a,
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
 
-#ifndef ULLM_GEMM_BSTAGES
-#define ULLM_GEMM_BSTAGES 2
-#endif
-
 template <uint32_t BM_, uint32_t BN_, uint32_t WM_, uint32_t WN_,
           uint32_t BSTAGES_ = 2, uint32_t ASTAGES_ = 2, bool PP_ = false>
 struct GemmCfg {
@@ -760,7 +756,12 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   }  // tiles
 }
 
-using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
+// 256 x 256: 2 waves of 128 rows x 4 of 64 columns, ping-pong with three B
+// stages (LDS 160 KiB; the epilogue chunks fit A stage 1 at 64 columns per
+// wave).  Measured on MI355X against the same block without the ping-pong
+// loop: M=2048 N=8192 54.5 against 57.5 us, M=4096 N=4096 53.1 against 56.8
+// us, M=2048 N=16384 110 against 116.4 us.
+using GemmLarge = GemmCfg<256, 256, 2, 4, 3, 2, true>;
 // 224 columns: 4 waves of 64 rows x 2 of 112 columns, ping-pong main loop.
 // For N = 28672 (and any N with whole 224-column blocks) the tile count
 // becomes a multiple of the CU count where 256-column tiles leave the last
@@ -770,14 +771,11 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, ULLM_GEMM_BSTAGES>;  // default
 // issue split between the groups (SPLIT): 196-197 against 207 us, 1.14
 // against 1.31 us per k-step; a third B stage with group 0 still issuing
 // every copy gained nothing.
-#ifndef ULLM_GEMM_PP_BSTAGES
-#define ULLM_GEMM_PP_BSTAGES 3
-#endif
-using GemmNarrow = GemmCfg<256, 224, 4, 2, ULLM_GEMM_PP_BSTAGES, 2, true>;
+using GemmNarrow = GemmCfg<256, 224, 4, 2, 3, 2, true>;
 // 192 columns: 4 waves of 64 rows x 2 of 96 columns, ping-pong, for grids
 // where it fills the last round (M = 2048, N = 6144: 256 tiles, one full
 // round; 48.5 against 54.1 us without the ping-pong loop).
-using GemmNarrow192 = GemmCfg<256, 192, 4, 2, ULLM_GEMM_PP_BSTAGES, 2, true>;
+using GemmNarrow192 = GemmCfg<256, 192, 4, 2, 3, 2, true>;
 // 8 waves of 64 x 32; 2 workgroups per CU.  The ping-pong loop measured
 // level or slower here (two workgroups already interleave on each SIMD)
 // and needs more than the 128 registers per wave two workgroups allow.
