@@ -826,16 +826,19 @@ bool gemm_use_mid(uint32_t m, uint32_t n, uint32_t cus) {
 }
 
 // Where the 128 x 128 blocks would win over the wide ones, 256 x 128 ping-pong
-// blocks (one workgroup per CU) win over them in turn when their grid needs
-// no more rounds and fills at least half of the CUs.  Measured on MI355X at
-// N = 4096: M=2048 K=4096 33.1 against 38.2 us, K=14336 100.6-101.2 against
-// 120.5-121.0 us, M=1024 K=4096 27.5 against 30.5 us.
+// blocks (one workgroup per CU) win over them in turn whenever their grid
+// needs no more rounds: one 256 x 128 tile takes less time than a round of
+// two 128 x 128 tiles per CU, even with most CUs idle.  Measured on MI355X at
+// K = 4096 (against 128 x 128): M=2048 N=4096 33.1 against 38.2 us (K=14336:
+// 100.6 against 120.5 us), M=1024 27.5 against 30.5, M=256 26.8 against 29.6
+// (16 tiles), M=512 N=6144 27.7 against 30.7, M=256 N=28672 43.3 against
+// 48.6 us.
 bool gemm_use_128(uint32_t m, uint32_t n, uint32_t cus) {
   const uint64_t t128 = uint64_t((m + 255) / 256) * ((n + 127) / 128);
   const uint64_t tmid = uint64_t((m + 127) / 128) * ((n + 127) / 128);
   const uint64_t r128 = (t128 + cus - 1) / cus;
   const uint64_t rmid = (tmid + 2 * cus - 1) / (2 * cus);
-  return r128 <= rmid && 2 * t128 >= cus;
+  return r128 <= rmid;
 }
 
 template <class C>
