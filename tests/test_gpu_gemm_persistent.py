@@ -33,11 +33,14 @@ PERSISTENT = [
     ("256x192", 250, 98304, 256),    # 512 tiles
     ("128x128", 1100, 14000, 256),   # 990 tiles on 512 workgroups, ragged N
 ]
-# One round of 256 x 128 ping-pong blocks (the N = 4096 prefill shapes): the
-# launch is not persistent, so only the block is asserted.
+# One round of 256-row ping-pong blocks (the N = 4096 and 6144 prefill
+# shapes, and a 256-column one) with several k-steps, so the three-stage B
+# ring wraps: the launch is not persistent, so only the block is asserted.
 ONE_ROUND = [
     ("256x128", 2048, 4096, 256),    # 256 tiles on 256 CUs
     ("256x128", 1024, 4000, 128),    # 128 tiles, ragged N
+    ("256x256", 2048, 8192, 512),    # 256 tiles, four k-steps
+    ("256x192", 2048, 6144, 384),    # 256 tiles, three k-steps
 ]
 CASES = [c + (True,) for c in PERSISTENT] + [c + (False,) for c in ONE_ROUND]
 
