@@ -190,6 +190,9 @@ struct GemmCfg {
   static constexpr uint32_t CHUNK_BASE = SPLIT ? A_BYTES : STAGE_BYTES;
   static_assert(!SPLIT || (ASTAGES == 2 && WAVES * CHUNK_BYTES <= A_BYTES),
                 "epilogue chunks fit A stage 1");
+  // The split loop waits for a step's B copies by count (each copying wave
+  // issues B_COPIES per step), so every copying wave must issue as many.
+  static_assert(!SPLIT || B_TILES % CW == 0, "B copies split evenly");
   static constexpr uint32_t LDS = SPLIT ? STAGE_BYTES : STAGE_BYTES + WAVES * CHUNK_BYTES;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
