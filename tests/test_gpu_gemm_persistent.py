@@ -38,9 +38,11 @@ PERSISTENT = [
 # ring wraps: the launch is not persistent, so only the block is asserted.
 ONE_ROUND = [
     ("256x128", 2048, 4096, 256),    # 256 tiles on 256 CUs
-    ("256x128", 1024, 4000, 128),    # 128 tiles, ragged N
+    ("256x64", 1024, 4000, 128),     # 252 tiles, ragged N
     ("256x256", 2048, 8192, 512),    # 256 tiles, four k-steps
     ("256x192", 2048, 6144, 384),    # 256 tiles, three k-steps
+    ("256x64", 256, 4096, 512),      # 64 tiles, the smallest grids
+    ("256x64", 300, 2000, 256),      # 64 tiles, ragged M and N
 ]
 CASES = [c + (True,) for c in PERSISTENT] + [c + (False,) for c in ONE_ROUND]
 

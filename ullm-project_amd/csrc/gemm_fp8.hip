@@ -787,6 +787,8 @@ using GemmMid = GemmCfg<128, 128, 2, 4>;
 // stages, one workgroup per CU, for N = 4096-class grids (one full round of
 // 256 x 128 tiles at M = 2048).
 using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 2, true>;
+// 64 columns: 4 waves of 64 rows x 2 of 32 columns, for the smallest grids.
+using GemmNarrow64 = GemmCfg<256, 64, 4, 2, 3, 2, true>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
@@ -842,6 +844,20 @@ bool gemm_use_128(uint32_t m, uint32_t n, uint32_t cus) {
   const uint64_t r128 = (t128 + cus - 1) / cus;
   const uint64_t rmid = (tmid + 2 * cus - 1) / (2 * cus);
   return r128 <= rmid;
+}
+
+// Among those, 256 x 64 blocks when their grid needs no more rounds than the
+// 256 x 128 one: on grids this small a tile's time is set by its k-loop, not
+// by its width.  Measured on MI355X at K = 4096 (against 256 x 128): M=256
+// N=4096 23.0 against 27.0 us, M=512 N=4096 23.6 against 27.0, M=256
+// N=6144 23.9 against 27.3, M=768 N=4096 25.2 against 27.4, M=1024 N=4096
+// 26.8 against 27.7 (K=14336: 83.0 against 85.2), M=256 N=14336 29.7
+// against 30.0.
+bool gemm_use_64(uint32_t m, uint32_t n, uint32_t cus) {
+  const uint64_t mb = (m + 255) / 256;
+  const uint64_t r64 = (mb * ((n + 63) / 64) + cus - 1) / cus;
+  const uint64_t r128 = (mb * ((n + 127) / 128) + cus - 1) / cus;
+  return r64 <= r128;
 }
 
 template <class C>
@@ -906,6 +922,7 @@ hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
     case kGemmNarrow: return launch_gemm_lds<GemmNarrow, EPI>(a, p, s);
     case kGemmNarrow192: return launch_gemm_lds<GemmNarrow192, EPI>(a, p, s);
     case kGemmNarrow128: return launch_gemm_lds<GemmNarrow128, EPI>(a, p, s);
+    case kGemmNarrow64: return launch_gemm_lds<GemmNarrow64, EPI>(a, p, s);
     case kGemmLarge: return launch_gemm_lds<GemmLarge, EPI>(a, p, s);
     default: break;
   }
@@ -939,9 +956,14 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
   const char *persist_env = tuning_env("ULLM_GEMM_PERSIST");
   const bool persist = persist_env == nullptr || persist_env[0] != '0';
   const int forced_bn = bn_env ? std::atoi(bn_env) : 0;
-  if (forced_bn == 128 ||
-      (forced_bn == 0 && cfg == nullptr && gemm_use_mid(m, n, cus) &&
-       gemm_use_128(m, n, cus))) {
+  const bool narrow = forced_bn == 0 && cfg == nullptr && gemm_use_mid(m, n, cus) &&
+                      gemm_use_128(m, n, cus);
+  if (forced_bn == 64 || (narrow && gemm_use_64(m, n, cus))) {
+    p.kind = kGemmNarrow64;
+    fill_plan<GemmNarrow64>(p, m, n, cus, persist);
+    return p;
+  }
+  if (forced_bn == 128 || narrow) {
     p.kind = kGemmNarrow128;
     fill_plan<GemmNarrow128>(p, m, n, cus, persist);
     return p;

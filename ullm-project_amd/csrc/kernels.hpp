@@ -92,6 +92,7 @@ enum GemmKind : uint32_t {
   kGemmNarrow192 = 3,   // LDS-pipelined 256 x 192
   kGemmMid = 4,         // LDS-pipelined 128 x 128, two workgroups per CU
   kGemmNarrow128 = 5,   // LDS-pipelined 256 x 128
+  kGemmNarrow64 = 6,    // LDS-pipelined 256 x 64
 };
 struct GemmPlan {
   uint32_t kind, block_m, block_n, tiles, grid;
