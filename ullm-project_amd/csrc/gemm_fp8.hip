@@ -182,18 +182,19 @@ struct GemmCfg {
   // operand stages (or in A stage 1, below), so the stages the next tile's
   // first copies fill stay free.
   static constexpr uint32_t CHUNK_BYTES = 16 * OUT_STRIDE * 2;
-  // Ping-pong with three B stages: waves 0-3 copy A one k-step ahead, waves
-  // 4-7 copy B two k-steps ahead, each in its own read phase, so the copy
-  // issue of a k-step is split over its two phases; the epilogue chunks
-  // then live in A stage 1, which the next tile's first copies leave alone.
-  static constexpr bool SPLIT = PP && BSTAGES == 3;
-  static constexpr uint32_t CHUNK_BASE = SPLIT ? A_BYTES : STAGE_BYTES;
-  static_assert(!SPLIT || (ASTAGES == 2 && WAVES * CHUNK_BYTES <= A_BYTES),
+  // The ping-pong loop runs with three B stages: waves 0-3 copy A one
+  // k-step ahead, waves 4-7 copy B two k-steps ahead, each in its own read
+  // phase, so the copy issue of a k-step is split over its two phases; the
+  // epilogue chunks then live in A stage 1, which the next tile's first
+  // copies leave alone.
+  static_assert(!PP || BSTAGES == 3, "ping-pong: three B stages");
+  static constexpr uint32_t CHUNK_BASE = PP ? A_BYTES : STAGE_BYTES;
+  static_assert(!PP || (ASTAGES == 2 && WAVES * CHUNK_BYTES <= A_BYTES),
                 "epilogue chunks fit A stage 1");
-  // The split loop waits for a step's B copies by count (each copying wave
-  // issues B_COPIES per step), so every copying wave must issue as many.
-  static_assert(!SPLIT || B_TILES % CW == 0, "B copies split evenly");
-  static constexpr uint32_t LDS = SPLIT ? STAGE_BYTES : STAGE_BYTES + WAVES * CHUNK_BYTES;
+  // The ping-pong loop waits for a step's B copies by count (each copying
+  // wave issues B_COPIES per step), so every copying wave must issue as many.
+  static_assert(!PP || B_TILES % CW == 0, "B copies split evenly");
+  static constexpr uint32_t LDS = PP ? STAGE_BYTES : STAGE_BYTES + WAVES * CHUNK_BYTES;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
 
@@ -337,10 +338,10 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       byte_buffer(a.xq, uint32_t(uint64_t(a.m) * a.ldxq));
   const __amdgpu_buffer_rsrc_t bbuf =
       byte_buffer(a.tiles, uint32_t(uint64_t(stripes) * a.units * 1024));
-  // With the ping-pong loop the first CW waves copy A, and B too unless
-  // the copies are split (then the last CW waves copy B).
+  // With the ping-pong loop the first CW waves copy A and the last CW B;
+  // otherwise every wave copies both.
   const bool a_copier = !C::PP || wave < C::CW;
-  const bool b_copier = !C::PP || (C::SPLIT ? wave >= C::CW : wave < C::CW);
+  const bool b_copier = !C::PP || wave >= C::CW;
   const uint32_t cwave = wave % C::CW;
   // Copies of step ks into the given stage (default: the ring slot of ks).
   auto copy_a_to = [&](uint32_t ks, char *st) {
@@ -411,53 +412,46 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   gemm_barrier();
 
   if constexpr (C::PP) {
-    static_assert(AAHEAD == 1 && (BAHEAD == 1 || C::SPLIT) && C::WAVES == 8,
-                  "ping-pong: two A stages, 8 waves");
+    static_assert(AAHEAD == 1 && C::WAVES == 8,
+                  "ping-pong: two A stages, three B stages, 8 waves");
     // Waves 0-3 (group 0) and 4-7 (group 1) sit one of each per SIMD, and
     // run the same loop -- read a step's operands from LDS, barrier, run
     // its MFMAs, barrier -- with group 1 one phase behind (an extra barrier
     // before its loop, matched by one after group 0's).  While one wave of
-    // a SIMD waits on LDS the other keeps the matrix core busy.  With two B
-    // stages group 0 issues all copies: those for step ks + 1 go out before
-    // it reads step ks (their stage was last read by group 1 in the phase
-    // just ended) and are waited for before the barrier that ends its MFMA
-    // phase, so they have landed before either group reads them.  With
-    // three (SPLIT) group 0 issues only A that way, and group 1 issues B
-    // for step ks + 2 before it reads step ks and waits for step ks + 1's B
-    // before the barrier that ends its read phase; each phase then carries
-    // about half of a step's copy instructions.  The copies slow the loop
-    // in proportion to the instructions issued in one phase, not by their
-    // latency (waiting for them costs ~1 %): on MI355X at M=2048,
-    // N=28672 the split took a k-step of every CU's tile from 1.31 to 1.14
-    // us (K sweep 4096 -> 8192) and the launch from 207 to 197 us.
+    // a SIMD waits on LDS the other keeps the matrix core busy.  Group 0
+    // issues the A copies for step ks + 1 before it reads step ks (their
+    // stage was last read by group 1 in the phase just ended) and waits for
+    // them before the barrier that ends its MFMA phase; group 1 issues the
+    // B copies for step ks + 2 (three B stages) before it reads step ks and
+    // waits for step ks + 1's before the barrier that ends its read phase.
+    // Each phase then carries about half of a step's copy instructions.
+    // The copies slow the loop in proportion to the instructions issued in
+    // one phase, not by their latency (waiting for them costs ~1 %): on
+    // MI355X at M=2048, N=28672, with group 0 issuing every copy into two B
+    // stages, a k-step of every CU's tile took 1.31 us (K sweep 4096 ->
+    // 8192) and the launch 207 us; split, 1.14 us and 197 us.
     const bool g1 = wave >= C::WAVES / 2;
     i32x8 af[C::TM], bf[C::TN];
     if (g1) {
       gemm_barrier();
     }
-    // The stages being read, kept as counters (A: ks % 2, B: ks % BSTAGES;
-    // bn: the B stage of step ks + 2 when B runs two steps ahead).
+    // The stages being read, kept as counters (A: ks % 2, B: ks % 3; bn:
+    // the B stage of step ks + 2).
     uint32_t st = 0, sb = 0, bn = 2;
     char *const bstages = lds + C::ASTAGES * C::A_BYTES;
 #pragma clang loop unroll(disable)
     for (uint32_t ks = 0; ks < ksteps; ++ks) {
-      if constexpr (C::SPLIT) {
-        // Group 0 copies A for step ks + 1 (its stage was last read in the
-        // phase just ended), group 1 B for step ks + 2 (its stage held
-        // step ks - 1, read by both groups before this phase).
-        if (!g1 && ks + 1 < ksteps) {
-          copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
-        }
-        if (g1 && ks + 2 < ksteps) {
-          copy_b_to(ks + 2, bstages + bn * C::B_BYTES);
-        }
-      } else if (ks + 1 < ksteps) {
+      // Group 0 copies A for step ks + 1 (its stage was last read in the
+      // phase just ended), group 1 B for step ks + 2 (its stage held step
+      // ks - 1, read by both groups before this phase).
+      if (!g1 && ks + 1 < ksteps) {
         copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
-        copy_b_to(ks + 1, bstages + (st ^ 1u) * C::B_BYTES);
+      }
+      if (g1 && ks + 2 < ksteps) {
+        copy_b_to(ks + 2, bstages + bn * C::B_BYTES);
       }
       const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
-      const char *Bs = bstages + (C::SPLIT ? sb : st) * C::B_BYTES +
-                       (wn * C::TN * 2) * 1024 + lane * 16;
+      const char *Bs = bstages + sb * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
       st ^= 1u;
       sb = sb == 2 ? 0u : sb + 1u;
       bn = bn == 2 ? 0u : bn + 1u;
@@ -469,16 +463,14 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       for (uint32_t j = 0; j < C::TN; ++j) {
         bf[j] = lds_operand(Bs + j * 2048);
       }
-      if constexpr (C::SPLIT) {
-        // Group 1: step ks + 1's B copies (issued a step ago) have landed
-        // before the barrier after which group 0 reads them; step ks + 2's
-        // stay in flight.
-        if (g1) {
-          if (ks + 2 < ksteps) {
-            wait_vm<C::B_COPIES>();
-          } else {
-            __builtin_amdgcn_s_waitcnt(0);
-          }
+      // Group 1: step ks + 1's B copies (issued a step ago) have landed
+      // before the barrier after which group 0 reads them; step ks + 2's
+      // stay in flight.
+      if (g1) {
+        if (ks + 2 < ksteps) {
+          wait_vm<C::B_COPIES>();
+        } else {
+          __builtin_amdgcn_s_waitcnt(0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -492,8 +484,8 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (!C::SPLIT || !g1) {
-        __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's A (and B) copies landed
+      if (!g1) {
+        __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's A copies have landed
       }
       gemm_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -771,7 +763,7 @@ using GemmLarge = GemmCfg<256, 256, 2, 4, 3, 2, true>;
 // round half empty.  Measured on MI355X at M=2048, N=28672: ping-pong
 // 215-220 against 232-235 us (per 128-deep k-step of every CU's tile 1.32
 // against 1.48-1.54 us, from a K sweep).  Three B stages with the copy
-// issue split between the groups (SPLIT): 196-197 against 207 us, 1.14
+// issue split between the groups: 196-197 against 207 us, 1.14
 // against 1.31 us per k-step; a third B stage with group 0 still issuing
 // every copy gained nothing.
 using GemmNarrow = GemmCfg<256, 224, 4, 2, 3, 2, true>;
