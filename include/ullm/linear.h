@@ -144,9 +144,10 @@ typedef struct ullm_linear_forward_desc_t {
   uint32_t activation_mode; /* ULLM_LINEAR_ACT_*, for BF16 x */
   float alpha;              /* output multiplier; 1.0f for a plain product */
   void *stream;
-  /* Device scratch (ullm_linear_workspace_size bytes) for ACT_FP8_PER_TOKEN
-   * and for split-K decode calls; null = library-owned.  For split-K calls
-   * it must be zero before its first use (each call leaves it so).  The
+  /* Device scratch (ullm_linear_workspace_size bytes) for prefill calls
+   * (FP8 GEMM) and for split-K decode calls; null = library-owned.  Its
+   * first 1 KiB holds split-K counters: zero it before the first use (every
+   * call leaves that region zero, and no call writes it otherwise).  The
    * library-owned buffers are one per device and stream (calls on one stream
    * share them in stream order) and are allocated, or grown, by the first
    * call that needs them: make that call outside stream capture.  A grown
@@ -230,7 +231,7 @@ typedef struct ullm_linear_plan_t {
   uint32_t block_n;
   uint32_t tiles;   /* GEMM: output tiles */
   uint32_t grid;    /* GEMM: workgroups; grid < tiles = persistent grid */
-  uint32_t split_k; /* GEMV: K parts per stripe group (1 = no split) */
+  uint32_t split_k; /* K parts per GEMV stripe group or GEMM tile (1 = no split) */
   uint32_t gemv_variant; /* GEMV: ULLM_LINEAR_GEMV_* (0 otherwise) */
   uint32_t gemv_waves;   /* GEMV: waves per workgroup */
   uint32_t gemv_stripes; /* GEMV: stripes sharing one activation load */
@@ -276,10 +277,11 @@ ULLM_HIP_API ullm_status_t ullm_linear_weight_dequantize(
 ULLM_HIP_API ullm_status_t ullm_linear_forward(
     const ullm_linear_forward_desc_t *desc, ullm_error_sink_t *error_sink);
 
-/* Bytes of workspace ullm_linear_forward needs for this descriptor: the
- * per-token activation quantization of the prefill path, or the split-K
- * scratch of a decode call that splits K (9 <= M <= 32, few output rows,
- * long K); 0 when the call needs none. */
+/* Bytes of workspace ullm_linear_forward needs for this descriptor: for the
+ * prefill GEMM the split-K counters and partial sums (grids of few output
+ * tiles split K over workgroups) and, for bf16 activations, their per-token
+ * quantization; for a decode call that splits K (9 <= M <= 32, few output
+ * rows, long K) its split-K scratch; 0 when the call needs none. */
 ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
     const ullm_linear_forward_desc_t *desc, uint64_t *bytes,
     ullm_error_sink_t *error_sink);
@@ -297,7 +299,7 @@ ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
  * Same descriptor, validation and result as ullm_linear_forward, except that
  * desc->workspace must be null: all scratch comes from a fixed per-device
  * array of 32 MiB held by the library for the life of the process (64 KiB of
- * split-K counters plus 32 MiB - 64 KiB for split-K partials or the prefill
+ * split-K counters plus 32 MiB - 64 KiB for split-K partials and the prefill
  * path's quantized activations, M*K + 4*M bytes each rounded up to 256).
  * Calls needing more are refused with ULLM_STATUS_UNSUPPORTED.  All calls on
  * one device share that array: calls that overlap in time on one device

@@ -71,7 +71,8 @@ def test_prefill_gemm_under_graph_with_caller_workspace(uh, gpu):
     lw = uh.LinearWeight.quantize(torch.from_numpy(weights(n, k, tag=7)).to(gpu),
                                   uh.ENCODING_FP8_E4M3_ROW)
     x = torch.randn(m, k, device=gpu).bfloat16()
-    ws = torch.empty(lw.workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN), dtype=torch.uint8,
+    # the first 1 KiB (split-K counters: this grid splits K) starts at zero
+    ws = torch.zeros(lw.workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN), dtype=torch.uint8,
                      device=gpu)
     y = torch.empty(m, n, device=gpu, dtype=torch.bfloat16)
     _replays_match(lambda: lw.forward(x, y, mode=uh.ACT_FP8_PER_TOKEN, workspace=ws), y)

@@ -354,19 +354,21 @@ def test_fp8_gemm_parity(uh, orc, gpu, m, n, k):
 
 
 def test_workspace_size_and_caller_workspace(uh, orc, gpu):
-    """Per-token FP8 prefill from bf16 needs M*K + 4M bytes (each part rounded
-    to 256); exact mode and pre-quantized input need none.  A caller-provided
-    workspace of that size gives the same result as the library buffer."""
+    """Per-token FP8 prefill from bf16 without a K split needs the 1 KiB
+    counter region plus M*K + 4*M bytes (each part rounded to 256); exact mode
+    and pre-quantized input need none.  A caller-provided workspace of that
+    size (counter region zeroed) gives the same result as the library
+    buffer."""
     m, n, k = 300, 64, 512
     q, s = orc.fp8_quantize_rows(weights(n, k, tag=41))
     lw = uh.LinearWeight.from_fp8(q, s)
     rup = lambda v: (v + 255) // 256 * 256
     need = lw.workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN)
-    assert need == rup(m * k) + rup(4 * m)
+    assert need == 1024 + rup(m * k) + rup(4 * m)
     assert lw.workspace_size(m) == 0
     assert lw.workspace_size(m, x_dtype=uh.DTYPE_F8E4M3FN) == 0
     x = to_torch_bf16(activations_bf16(orc, m, k, tag=42), gpu)
-    wsb = torch.empty((need,), dtype=torch.uint8, device=gpu)
+    wsb = torch.zeros((need,), dtype=torch.uint8, device=gpu)
     y1 = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN, workspace=wsb)
     y2 = lw.forward(x, out_dtype=torch.float32, mode=uh.ACT_FP8_PER_TOKEN)
     assert torch.equal(y1, y2)

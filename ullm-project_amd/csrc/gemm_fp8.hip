@@ -61,6 +61,12 @@ struct GemmArgs {
   bool y_f32;
   bool y_vec;  // bf16 rows 16-byte aligned: coalesced epilogue stores
   Epilogue epi;
+  // Split K (ping-pong blocks on grids of few tiles): K parts per tile, a
+  // counter per tile (zero on entry, left zero) and the fp32 partial sums.
+  uint32_t ksplit;
+  uint32_t *cnt;
+  float *part;
+  uint32_t part_bytes;
 };
 
 // 256 threads, block tile 64 (m) x 64 (n); wave (wm, wn) owns 32 x 32.
@@ -214,6 +220,9 @@ __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc,
       voff, soff, 0, 0);
 }
 
+// Cache policy of the split-K partial sums: sc0 | sc1 (system coherent).
+constexpr int kScGemm = 1 | 16;
+
 // Barrier without the fence of __syncthreads: LDS reads of this wave are
 // complete (lgkmcnt 0); the caller has already waited for its copies.
 __device__ __forceinline__ void gemm_barrier() {
@@ -291,9 +300,14 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   // evenly each XCD gets a contiguous range of tiles, so the workgroups
   // sharing one L2 also share operand tiles, and with a grid that is a
   // multiple of 8 every id of one workgroup stays on its XCD.
-  const uint32_t total = mblocks * nblocks;
+  // Work items: (tile, K part); without a split one per tile.
+  const uint32_t ksplit = C::PP ? a.ksplit : 1u;
+  const uint32_t total = mblocks * nblocks * ksplit;
   const uint32_t stripes = (a.n + 15) / 16;
   const uint32_t ksteps = a.k / C::BK;
+  // K part of the current item: steps k0 .. k0 + nk - 1.
+  const uint32_t kpp = (ksteps + ksplit - 1) / ksplit;
+  uint32_t ctile = 0, kp = 0, k0 = 0, nk = ksteps;
   const uint32_t wm = wave / C::WN, wn = wave % C::WN;
 
   // Per-lane copy sources of the current tile, loop-invariant within it: a
@@ -304,7 +318,12 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   uint32_t aoff[C::A_COPIES], boff[C::B_COPIES];
   uint32_t m0 = 0, T0 = 0;
   auto setup = [&](uint32_t id) {
-    const uint32_t tile = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
+    const uint32_t item = total % 8 == 0 ? (id % 8) * (total / 8) + id / 8 : id;
+    const uint32_t tile = item / ksplit;
+    ctile = tile;
+    kp = item % ksplit;
+    k0 = kp * kpp;
+    nk = min(ksteps, k0 + kpp) - k0;
     const uint32_t bm = tile % mblocks, bn = tile / mblocks;
     m0 = bm * C::BM;
     T0 = bn * (C::BN / 16);
@@ -368,17 +387,19 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   auto copy_b = [&](uint32_t ks) { copy_b_to(ks, b_buf(ks)); };
   constexpr uint32_t BAHEAD = C::BSTAGES - 1;  // k-steps B runs ahead
   constexpr uint32_t AAHEAD = C::ASTAGES - 1;  // k-steps A runs ahead
+  // The first copies of the item's K part (absolute steps k0 ..) into the
+  // first stages.
   auto prologue = [&]() {
 #pragma unroll
     for (uint32_t b = 0; b < AAHEAD; ++b) {
-      if (b < ksteps) {
-        copy_a(b);
+      if (b < nk) {
+        copy_a_to(k0 + b, a_buf(b));
       }
     }
 #pragma unroll
     for (uint32_t b = 0; b < BAHEAD; ++b) {
-      if (b < ksteps) {
-        copy_b(b);
+      if (b < nk) {
+        copy_b_to(k0 + b, b_buf(b));
       }
     }
   };
@@ -440,15 +461,16 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     uint32_t st = 0, sb = 0, bn = 2;
     char *const bstages = lds + C::ASTAGES * C::A_BYTES;
 #pragma clang loop unroll(disable)
-    for (uint32_t ks = 0; ks < ksteps; ++ks) {
+    for (uint32_t ks = 0; ks < nk; ++ks) {
       // Group 0 copies A for step ks + 1 (its stage was last read in the
       // phase just ended), group 1 B for step ks + 2 (its stage held step
-      // ks - 1, read by both groups before this phase).
-      if (!g1 && ks + 1 < ksteps) {
-        copy_a_to(ks + 1, lds + (st ^ 1u) * C::A_BYTES);
+      // ks - 1, read by both groups before this phase); ks counts the
+      // item's K part, k0 + ks is the absolute step.
+      if (!g1 && ks + 1 < nk) {
+        copy_a_to(k0 + ks + 1, lds + (st ^ 1u) * C::A_BYTES);
       }
-      if (g1 && ks + 2 < ksteps) {
-        copy_b_to(ks + 2, bstages + bn * C::B_BYTES);
+      if (g1 && ks + 2 < nk) {
+        copy_b_to(k0 + ks + 2, bstages + bn * C::B_BYTES);
       }
       const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
       const char *Bs = bstages + sb * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
@@ -467,7 +489,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       // before the barrier after which group 0 reads them; step ks + 2's
       // stay in flight.
       if (g1) {
-        if (ks + 2 < ksteps) {
+        if (ks + 2 < nk) {
           wait_vm<C::B_COPIES>();
         } else {
           __builtin_amdgcn_s_waitcnt(0);
@@ -558,6 +580,81 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   }
 
   // The main loop ended on a barrier: every operand stage is free.
+  if constexpr (C::PP) {
+    if (ksplit > 1) {
+      // Split K: every part stores its fp32 sums; the last part of the tile
+      // to arrive adds all parts in part order (the result does not depend
+      // on the arrival order) and runs the epilogue, the others move on.
+      // The parts of a tile may run on different XCDs, whose L2 caches are
+      // not coherent: the sums are stored and loaded with the
+      // system-coherent policy (sc0 sc1: to and from memory, never a stale
+      // L2 line), the stores complete (vmcnt 0) before this workgroup's
+      // device-scope counter increment, and the counter elects the one
+      // workgroup that saw every other part's increment, so every other
+      // part's stores had completed before it loads them.  The finisher
+      // resets the counter for the next call.
+      const __amdgpu_buffer_rsrc_t pbuf = byte_buffer(a.part, a.part_bytes);
+      constexpr uint32_t WB = C::TM * C::TN * kWave * 16;  // bytes per wave and part
+      const uint32_t lane_off = wave * WB + lane * 16;
+      const uint32_t part0 = ctile * ksplit * (C::WAVES * WB);
+#pragma unroll
+      for (uint32_t i = 0; i < C::TM; ++i) {
+#pragma unroll
+        for (uint32_t j = 0; j < C::TN; ++j) {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, acc[i][j]), pbuf,
+              part0 + kp * (C::WAVES * WB) + lane_off + (i * C::TN + j) * (kWave * 16), 0,
+              kScGemm);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores completed
+      gemm_barrier();
+      // The flag lives in B stage 2, which no copy targets until the next
+      // item's prologue (issued below, after the flag is read).
+      uint32_t *flag = reinterpret_cast<uint32_t *>(lds + C::ASTAGES * C::A_BYTES +
+                                                    2 * C::B_BYTES);
+      if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(a.cnt + ctile, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev + 1 == ksplit;
+        if (last) {
+          __hip_atomic_store(a.cnt + ctile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        *flag = last ? 1u : 0u;
+      }
+      gemm_barrier();
+      if (__builtin_amdgcn_readfirstlane(*flag) == 0u) {
+        const uint32_t nxt = id + gridDim.x;
+        if (nxt >= total) {
+          break;
+        }
+        id = nxt;
+        gemm_barrier();  // every wave has read the flag
+        setup(id);
+        prologue();
+        continue;
+      }
+#pragma unroll
+      for (uint32_t i = 0; i < C::TM; ++i) {
+#pragma unroll
+        for (uint32_t j = 0; j < C::TN; ++j) {
+          f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (uint32_t q = 0; q < ksplit; ++q) {
+            const f32x4 t =
+                q == kp ? acc[i][j]
+                        : __builtin_bit_cast(
+                              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         pbuf,
+                                         part0 + q * (C::WAVES * WB) + lane_off +
+                                             (i * C::TN + j) * (kWave * 16),
+                                         0, kScGemm));
+            v += t;
+          }
+          acc[i][j] = v;
+        }
+      }
+    }
+  }
   const uint32_t cm0 = m0, cT0 = T0;
   const uint32_t next = id + gridDim.x;
   const bool more = next < total;
@@ -852,6 +949,43 @@ bool gemm_use_64(uint32_t m, uint32_t n, uint32_t cus) {
   return r64 <= r128;
 }
 
+// Split K over workgroups on grids of few tiles (ping-pong blocks, one round,
+// at most half of the CUs busy): a 256-row tile's k-loop takes ~0.7 us per
+// 128-deep step however little each step holds, so the idle CUs take parts
+// of K, at least 16 steps each, and the last part of a tile to finish adds
+// the parts.  ULLM_GEMM_SPLIT=0 (read only by a -DULLM_TUNING build) turns
+// it off.
+void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
+  p.ksplit = 1;
+  const char *env = tuning_env("ULLM_GEMM_SPLIT");
+  if ((env != nullptr && env[0] == '0') || p.grid < p.tiles) {
+    return;
+  }
+  // A part of fewer than 16 k-steps does not pay for its partial-sum round
+  // trip (store, counter, reload by the finisher): with 8 the measured
+  // M=300 N=2000 K=2048 launch took 14.3 us split against 14.0 unsplit.
+  uint32_t min_steps = 16;
+  if (const char *v = tuning_env("ULLM_GEMM_SPLIT_STEPS")) {
+    min_steps = std::max(1, std::atoi(v));
+  }
+  const uint32_t ksteps = k / 128;
+  if (ksteps < 2 * min_steps || 2 * p.tiles > cus ||
+      p.tiles * 4 > kGemmCounterBytes) {
+    return;
+  }
+  uint32_t ks = std::min(cus / p.tiles, ksteps / min_steps);
+  // Every part holds at least one step.
+  while (ks > 1 && (ks - 1) * ((ksteps + ks - 1) / ks) >= ksteps) {
+    --ks;
+  }
+  const uint64_t part = uint64_t(p.tiles) * ks * p.block_m * p.block_n * 4;
+  if (ks < 2 || part >= (uint64_t(1) << 31)) {
+    return;
+  }
+  p.ksplit = ks;
+  p.grid = p.tiles * ks;
+}
+
 template <class C>
 void fill_plan(GemmPlan &p, uint32_t m, uint32_t n, uint32_t cus,
                bool persist) {
@@ -933,6 +1067,7 @@ hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
 GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
                        bool offsets_fit, uint32_t cus) {
   GemmPlan p{};
+  p.ksplit = 1;
   if (!(vec && offsets_fit && k % 128 == 0)) {
     p.kind = kGemmDirect;
     p.block_m = 64;
@@ -953,11 +1088,13 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
   if (forced_bn == 64 || (narrow && gemm_use_64(m, n, cus))) {
     p.kind = kGemmNarrow64;
     fill_plan<GemmNarrow64>(p, m, n, cus, persist);
+    plan_split(p, k, cus);
     return p;
   }
   if (forced_bn == 128 || narrow) {
     p.kind = kGemmNarrow128;
     fill_plan<GemmNarrow128>(p, m, n, cus, persist);
+    plan_split(p, k, cus);
     return p;
   }
   if ((cfg != nullptr && cfg[0] == 'm') ||
@@ -974,13 +1111,33 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
     case 192: p.kind = kGemmNarrow192; fill_plan<GemmNarrow192>(p, m, n, cus, persist); break;
     default: p.kind = kGemmLarge; fill_plan<GemmLarge>(p, m, n, cus, persist); break;
   }
+  plan_split(p, k, cus);
   return p;
 }
 
+GemmPlan plan_fp8_gemm_call(const void *xq, uint64_t ldxq,
+                            const ullm_linear_weight_t *w, uint32_t m) {
+  const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
+  const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
+                           w->fp8.bytes() < (uint64_t(1) << 32);
+  return plan_fp8_gemm(m, static_cast<uint32_t>(w->n), static_cast<uint32_t>(w->k),
+                       vec, offsets_fit, device_cu_count());
+}
+
+uint64_t gemm_split_bytes(const GemmPlan &p) {
+  return p.ksplit > 1
+             ? kGemmCounterBytes + uint64_t(p.tiles) * p.ksplit * p.block_m * p.block_n * 4
+             : 0;
+}
+
+// `p` is plan_fp8_gemm_call for the same xq, ldxq, w and m; with a split,
+// `cnt` points at kGemmCounterBytes of counters (zero) and `part` at
+// gemm_split_bytes(p) - kGemmCounterBytes bytes for the partial sums.
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            const ullm_linear_weight_t *w, uint32_t m, void *y,
                            uint64_t ldy, bool y_f32, float alpha,
-                           const Epilogue &epi, hipStream_t s) {
+                           const Epilogue &epi, const GemmPlan &p, uint32_t *cnt,
+                           float *part, hipStream_t s) {
   GemmArgs a{};
   a.xq = xq;
   a.xs = xs;
@@ -997,10 +1154,16 @@ hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
   a.y_f32 = y_f32;
   a.y_vec = reinterpret_cast<uintptr_t>(y) % 16 == 0 && ldy % 8 == 0;
   a.epi = epi;
+  a.ksplit = p.ksplit;
+  if (p.ksplit > 1) {
+    if (cnt == nullptr || part == nullptr) {
+      return hipErrorInvalidValue;
+    }
+    a.cnt = cnt;
+    a.part = part;
+    a.part_bytes = static_cast<uint32_t>(gemm_split_bytes(p) - kGemmCounterBytes);
+  }
   const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
-  const bool offsets_fit = uint64_t(m) * ldxq < (uint64_t(1) << 32) &&
-                           w->fp8.bytes() < (uint64_t(1) << 32);
-  const GemmPlan p = plan_fp8_gemm(m, a.n, a.k, vec, offsets_fit, device_cu_count());
   switch (epi.kind) {
     case kEpiSiluMul: return gemm_e<kEpiSiluMul>(a, p, vec, s);
     case kEpiResidual: return gemm_e<kEpiResidual>(a, p, vec, s);

@@ -96,6 +96,7 @@ enum GemmKind : uint32_t {
 };
 struct GemmPlan {
   uint32_t kind, block_m, block_n, tiles, grid;
+  uint32_t ksplit;  // K parts per tile (1: no split); grid = tiles * ksplit
 };
 // The kernel and grid launch_fp8_gemm takes for an M x N x K product on a
 // device of `cus` compute units (vec: activation rows 16-byte aligned;
@@ -103,6 +104,14 @@ struct GemmPlan {
 // persistent grid, each workgroup walking several tiles.
 GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
                        bool offsets_fit, uint32_t cus);
+// The plan of a prefill call on the weight's device (xq: the quantized
+// activations as the GEMM reads them, row stride ldxq bytes).
+GemmPlan plan_fp8_gemm_call(const void *xq, uint64_t ldxq,
+                            const ullm_linear_weight_t *w, uint32_t m);
+// Split-K scratch of a plan: a counter region of kGemmCounterBytes (zero on
+// entry, left zero) followed by the partial sums; 0 when it does not split.
+constexpr uint64_t kGemmCounterBytes = 1024;
+uint64_t gemm_split_bytes(const GemmPlan &p);
 
 // ------------------------------------------------------------ host helpers
 // Fixed device scratch of the allocation-free forward: a counter region

@@ -28,7 +28,8 @@ namespace ullm {
 hipError_t launch_fp8_gemm(const uint8_t *xq, const float *xs, uint64_t ldxq,
                            const ullm_linear_weight_t *w, uint32_t m,
                            void *y, uint64_t ldy, bool y_f32, float alpha,
-                           const Epilogue &epi, hipStream_t s);
+                           const Epilogue &epi, const GemmPlan &p, uint32_t *cnt,
+                           float *part, hipStream_t s);
 }  // namespace ullm
 
 namespace {
@@ -470,8 +471,26 @@ ullm_status_t validate_forward(const ullm_linear_forward_desc_t *d,
   return ULLM_STATUS_OK;
 }
 
-uint64_t prefill_workspace_bytes(uint64_t m, uint64_t k) {
-  return ullm::round_up(m * k, 256) + ullm::round_up(m * sizeof(float), 256);
+// Prefill scratch: the split-K counter region (zero; prefill calls that do
+// not split leave it alone), the split-K partial sums, then (for bf16
+// activations) the quantized activations and their scales.
+uint64_t prefill_split_bytes(const ullm::GemmPlan &p) {
+  const uint64_t split = ullm::gemm_split_bytes(p);
+  return split != 0 ? split : ullm::kGemmCounterBytes;
+}
+uint64_t prefill_workspace_bytes(uint64_t m, uint64_t k, const ullm::GemmPlan &p) {
+  return prefill_split_bytes(p) + ullm::round_up(m * k, 256) +
+         ullm::round_up(m * sizeof(float), 256);
+}
+// The GEMM plan of a prefill call; quantized activations in the workspace
+// sit at a 256-byte multiple past its start.
+ullm::GemmPlan prefill_plan(const ullm_linear_forward_desc_t *desc) {
+  const ullm_linear_weight_t *w = desc->weight;
+  const uint64_t ldx = desc->x_row_stride ? desc->x_row_stride : w->k;
+  const bool prequant = desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN;
+  const void *xq = prequant ? desc->x : desc->workspace;  // null: library-owned
+  return ullm::plan_fp8_gemm_call(xq, prequant ? ldx : w->k, w,
+                                  static_cast<uint32_t>(desc->m));
 }
 
 }  // namespace
@@ -682,7 +701,9 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_workspace_size(
                           desc->activation_mode == ULLM_LINEAR_ACT_FP8_PER_TOKEN;
     const ullm_linear_weight_t *w = desc->weight;
     if (quantize) {
-      *bytes = prefill_workspace_bytes(desc->m, w->k);
+      *bytes = desc->m == 0 ? 0 : prefill_workspace_bytes(desc->m, w->k, prefill_plan(desc));
+    } else if (desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN && desc->m != 0) {
+      *bytes = ullm::gemm_split_bytes(prefill_plan(desc));
     } else if (desc->x_dtype == ULLM_LINEAR_DTYPE_BF16 && desc->m != 0) {
       // Decode: split-K scratch when the launch would split K.
       const bool fp8w = w->encoding == ULLM_LINEAR_ENCODING_FP8_E4M3_ROW;
@@ -750,23 +771,17 @@ extern "C" ULLM_HIP_API ullm_status_t ullm_linear_forward_plan(
       plan->gemv_row_classes = c.classes;
       return ULLM_STATUS_OK;
     }
-    // The prefill path quantizes into a dense [M][K] workspace; pre-quantized
-    // activations keep the caller's pointer and stride.
-    const bool prequant = desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN;
-    const uint64_t ldxq = prequant ? ldx : w->k;
-    const void *xq = prequant ? desc->x : desc->workspace;  // null: library-owned
-    const bool vec = reinterpret_cast<uintptr_t>(xq) % 16 == 0 && ldxq % 16 == 0;
-    const bool offsets_fit = desc->m * ldxq < (uint64_t(1) << 32) &&
-                             w->fp8.bytes() < (uint64_t(1) << 32);
-    const ullm::GemmPlan p = ullm::plan_fp8_gemm(
-        static_cast<uint32_t>(desc->m), static_cast<uint32_t>(w->n),
-        static_cast<uint32_t>(w->k), vec, offsets_fit, ullm::device_cu_count());
+    // The prefill path quantizes into the workspace (256-byte aligned past
+    // its start); pre-quantized activations keep the caller's pointer and
+    // stride.
+    const ullm::GemmPlan p = prefill_plan(desc);
     plan->kernel = p.kind == ullm::kGemmDirect ? ULLM_LINEAR_KERNEL_GEMM_DIRECT
                                                : ULLM_LINEAR_KERNEL_GEMM_LDS;
     plan->block_m = p.block_m;
     plan->block_n = p.block_n;
     plan->tiles = p.tiles;
     plan->grid = p.grid;
+    plan->split_k = p.ksplit;
     return ULLM_STATUS_OK;
   });
 }
@@ -880,37 +895,53 @@ ullm_status_t forward_dispatch(const ullm_linear_forward_desc_t *desc,
     return ULLM_STATUS_OK;
   }
 
-  // FP8 activations on the FP8 matrix cores.
+  // FP8 activations on the FP8 matrix cores.  Scratch layout: split-K
+  // counters (zero on entry, left zero), split-K partial sums, then the
+  // quantized activations and their scales when x is bf16.
+  const bool prequant = desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN;
+  const ullm::GemmPlan plan = prefill_plan(desc);
+  const uint64_t split = ullm::gemm_split_bytes(plan);
+  const uint64_t head = prequant ? split : prefill_split_bytes(plan);
+  const uint64_t need = prequant ? split : prefill_workspace_bytes(desc->m, w->k, plan);
+  char *ws = nullptr;       // the scratch past the counter region
+  void *counters = nullptr;  // the counter region
+  if (need != 0) {
+    if (fixed != nullptr) {
+      if (need - ullm::kGemmCounterBytes > fs.bytes ||
+          ullm::kGemmCounterBytes > fs.counter_bytes) {
+        return write_errorf(error_sink, ULLM_STATUS_UNSUPPORTED,
+                            "this call needs " + std::to_string(need) +
+                                " bytes of prefill scratch; the fixed scratch holds " +
+                                std::to_string(fs.bytes));
+      }
+      counters = fs.counters;
+      ws = fs.base;
+    } else {
+      void *buf = desc->workspace;
+      if (buf != nullptr) {
+        if (desc->workspace_size < need) {
+          return write_errorf(error_sink, ULLM_STATUS_BUFFER_TOO_SMALL,
+                              "workspace needs " + std::to_string(need) + " bytes");
+        }
+      } else {
+        const ullm_status_t st =
+            library_workspace(w->device, desc->stream, true, need, &buf, error_sink);
+        if (st != ULLM_STATUS_OK) {
+          return st;
+        }
+      }
+      counters = buf;
+      ws = static_cast<char *>(buf) + ullm::kGemmCounterBytes;
+    }
+  }
   const uint8_t *xq = nullptr;
   const float *xs = nullptr;
   uint64_t ldxq = ldx;
-  if (desc->x_dtype == ULLM_LINEAR_DTYPE_F8E4M3FN) {
+  if (prequant) {
     xq = static_cast<const uint8_t *>(desc->x);
     xs = desc->x_scales;
   } else {
-    const uint64_t need = prefill_workspace_bytes(desc->m, w->k);
-    void *ws = desc->workspace;
-    if (fixed != nullptr) {
-      if (need > fs.bytes) {
-        return write_errorf(error_sink, ULLM_STATUS_UNSUPPORTED,
-                            "this call needs " + std::to_string(need) +
-                                " bytes of activation scratch; the fixed scratch holds " +
-                                std::to_string(fs.bytes));
-      }
-      ws = fs.base;
-    } else if (ws != nullptr) {
-      if (desc->workspace_size < need) {
-        return write_errorf(error_sink, ULLM_STATUS_BUFFER_TOO_SMALL,
-                            "workspace needs " + std::to_string(need) + " bytes");
-      }
-    } else {
-      const ullm_status_t st =
-          library_workspace(w->device, desc->stream, false, need, &ws, error_sink);
-      if (st != ULLM_STATUS_OK) {
-        return st;
-      }
-    }
-    uint8_t *wq = static_cast<uint8_t *>(ws);
+    uint8_t *wq = reinterpret_cast<uint8_t *>(ws) + (head - ullm::kGemmCounterBytes);
     float *wsc = reinterpret_cast<float *>(wq + ullm::round_up(desc->m * w->k, 256));
     HIP_TRY(error_sink, "activation quantize kernel",
             ullm::launch_act_quant(static_cast<const uint16_t *>(desc->x), ldx,
@@ -921,7 +952,9 @@ ullm_status_t forward_dispatch(const ullm_linear_forward_desc_t *desc,
   }
   HIP_TRY(error_sink, "fp8 gemm kernel",
           ullm::launch_fp8_gemm(xq, xs, ldxq, w, static_cast<uint32_t>(desc->m),
-                                desc->y, ldy, y_f32, desc->alpha, epi, s));
+                                desc->y, ldy, y_f32, desc->alpha, epi, plan,
+                                static_cast<uint32_t *>(counters),
+                                reinterpret_cast<float *>(ws), s));
   return ULLM_STATUS_OK;
 }
 
