@@ -13,7 +13,7 @@ average duration is timed with HIP events on the stream the kernels run on.
 Extra configurations (FP8 matvec, the FP8 small-M sweep M = 1..32 over the
 four Llama-3-8B layer shapes, a plain streaming-read floor at the headline
 sizes, the M=2048 FP8 GEMM and the 32-layer AQ4 decode stack; "gemm_shapes"
-adds the other prefill projections and M < 128, "vendor_gemm" the same FP8
+adds the other prefill projections, short prompts (M = 256, 512) and M < 128, "vendor_gemm" the same FP8
 GEMM through hipBLASLt for reference) are reported under "configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
@@ -409,9 +409,11 @@ def main():
         except Exception as exc:  # the vendor path is informational only
             log(f"vendor gemm unavailable: {exc}")
     if "gemm_shapes" in want:
-        # The other prefill projections, and M below one 128-row block.
+        # The other prefill projections, short prompts whose grids split K
+        # over workgroups, and M below one 128-row block.
         for m, n, k in ((2048, 6144, 4096), (2048, 4096, 4096),
-                        (2048, 4096, 14336), (64, 4096, 4096),
+                        (2048, 4096, 14336), (256, 4096, 4096),
+                        (512, 4096, 14336), (64, 4096, 4096),
                         (64, 28672, 4096), (120, 14336, 4096)):
             res = bench_gemm(r, m, n, k, max(3, args.steps // 10), 1)
             configs[f"fp8_gemm_m{m}_k{k}_n{n}"] = res
