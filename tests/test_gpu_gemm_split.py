@@ -28,6 +28,9 @@ SPLIT = [
     (300, 2000, 4224, 2),    # 33 k-steps: parts of 17 and 16
     (256, 1024, 8320, 4),    # 65 k-steps: parts of 17, 17, 17 and 14
     (256, 256, 4096, 2),     # 4 tiles
+    (256, 4480, 6144, 3),    # 70 tiles, 48 k-steps: three parts of 16
+    (256, 2048, 14336, 7),   # 32 tiles, 112 k-steps: seven parts of 16
+    (256, 2048, 14208, 6),   # 111 k-steps: five parts of 19 and one of 16
 ]
 
 
@@ -127,3 +130,40 @@ def test_split_gemm_caller_workspace(uh, orc, gpu):
     assert int(ws[:1024].count_nonzero()) == 0   # counters left zero
     # pre-quantized input needs only the split scratch
     assert lw.workspace_size(m, x_dtype=uh.DTYPE_F8E4M3FN) == 1024 + parts
+
+
+def test_split_plan_invariants(uh, gpu):
+    """Every plan over a sweep of prefill shapes: a split has at least two
+    parts of at least 16 k-steps each (none empty), one workgroup per part,
+    at most one round of the CUs, counters within their 1 KiB region, and the
+    workspace size that holds its partial sums."""
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    rup = lambda v: (v + 255) // 256 * 256
+    seen = set()
+    for n, k in ((256, 4096), (2000, 4096), (4096, 14336), (4480, 6144),
+                 (6144, 2048), (28672, 4096), (1024, 8320)):
+        lw = uh.LinearWeight.quantize(torch.zeros((n, k), device=gpu),
+                                      uh.ENCODING_FP8_E4M3_ROW)
+        for m in (33, 64, 128, 200, 256, 300, 512, 768, 1024, 2048):
+            x = torch.empty((m, k), dtype=torch.bfloat16, device=gpu)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+            p = lw.plan(x, y, mode=uh.ACT_FP8_PER_TOKEN)
+            need = lw.workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN)
+            steps = k // 128
+            if p.split_k > 1:
+                seen.add(p.split_k)
+                kpp = -(-steps // p.split_k)
+                assert p.kernel == uh.KERNEL_GEMM_LDS
+                assert p.block_m == 256, (m, n, k, p.block_m)
+                assert kpp >= 16 and (p.split_k - 1) * kpp < steps, (m, n, k, p.split_k)
+                assert p.grid == p.tiles * p.split_k <= cus, (m, n, k, p.grid)
+                assert p.tiles * 4 <= 1024
+                parts = p.tiles * p.split_k * p.block_m * p.block_n * 4
+                assert parts < 2 ** 31
+            else:
+                assert p.split_k == 1
+                parts = 0
+            assert need == 1024 + parts + rup(m * k) + rup(4 * m), (m, n, k, need)
+        lw.destroy()
+    if cus == 256:
+        assert seen >= {2, 3, 4}, seen
