@@ -14,7 +14,7 @@ Extra configurations (FP8 matvec, the FP8 small-M sweep M = 1..32 over the
 four Llama-3-8B layer shapes, a plain streaming-read floor at the headline
 sizes, the M=2048 FP8 GEMM and the 32-layer AQ4 decode stack; "gemm_shapes"
 adds the other prefill projections, short prompts (M = 256, 512) and M < 128, "vendor_gemm" the same FP8
-GEMM through hipBLASLt for reference) are reported under "configs".  The CPU
+GEMMs through hipBLASLt for reference) are reported under "configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
 
@@ -418,6 +418,13 @@ def main():
             res = bench_gemm(r, m, n, k, max(3, args.steps // 10), 1)
             configs[f"fp8_gemm_m{m}_k{k}_n{n}"] = res
             log("gemm", m, n, k, res["us_per_launch"])
+            if "vendor_gemm" in want:
+                try:
+                    v = bench_vendor_gemm(r, m, n, k, max(3, args.steps // 10), 1)
+                    configs[f"vendor_fp8_gemm_m{m}_k{k}_n{n}"] = v
+                    log("vendor gemm", m, n, k, v["us_per_launch"])
+                except Exception as exc:  # informational only
+                    log(f"vendor gemm {m} {n} {k} unavailable: {exc}")
 
     cpu = cpu_baseline(args.cpu_seconds)
     us = head["us_per_launch"]

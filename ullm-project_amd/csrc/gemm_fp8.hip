@@ -159,9 +159,12 @@ struct GemmCfg {
   // A (activations, L2-resident) is double-buffered; B (weights, streamed
   // from HBM) may get a third buffer so its copies run two k-steps ahead.
   static constexpr uint32_t BSTAGES = BSTAGES_;
-  // A third A buffer lets the activation copies run two k-steps ahead
-  // (measured slower on MI355X at M=2048, N=28672, K=4096: 264-270 against
-  // 250-252 us, so the copies are not waiting on latency).
+  // A third A buffer lets the activation copies run two k-steps ahead.
+  // Measured slower on MI355X in the 256 x 256 block before the ping-pong
+  // loop at M=2048, N=28672, K=4096 (264-270 against 250-252 us: the copies
+  // were not waiting on latency there), faster in the ping-pong 256 x 128
+  // and 256 x 64 blocks, whose grids of at most a few rounds leave each CU
+  // waiting on its copies (below).
   static constexpr uint32_t ASTAGES = ASTAGES_;
   static_assert(ASTAGES >= 2 && ASTAGES <= 3 && BSTAGES >= 2 && BSTAGES <= 3,
                 "one or two k-steps of look-ahead");
@@ -193,10 +196,12 @@ struct GemmCfg {
   // phase, so the copy issue of a k-step is split over its two phases; the
   // epilogue chunks then live in A stage 1, which the next tile's first
   // copies leave alone.
+  // With a third A stage (A copied two k-steps ahead too) the chunks move
+  // to A stage 2: the next tile's first copies fill A stages 0 and 1.
   static_assert(!PP || BSTAGES == 3, "ping-pong: three B stages");
-  static constexpr uint32_t CHUNK_BASE = PP ? A_BYTES : STAGE_BYTES;
-  static_assert(!PP || (ASTAGES == 2 && WAVES * CHUNK_BYTES <= A_BYTES),
-                "epilogue chunks fit A stage 1");
+  static constexpr uint32_t CHUNK_BASE = PP ? (ASTAGES - 1) * A_BYTES : STAGE_BYTES;
+  static_assert(!PP || WAVES * CHUNK_BYTES <= A_BYTES,
+                "epilogue chunks fit the last A stage");
   // The ping-pong loop waits for a step's B copies by count (each copying
   // wave issues B_COPIES per step), so every copying wave must issue as many.
   static_assert(!PP || B_TILES % CW == 0, "B copies split evenly");
@@ -433,8 +438,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   gemm_barrier();
 
   if constexpr (C::PP) {
-    static_assert(AAHEAD == 1 && C::WAVES == 8,
-                  "ping-pong: two A stages, three B stages, 8 waves");
+    static_assert(C::WAVES == 8, "ping-pong: 8 waves");
     // Waves 0-3 (group 0) and 4-7 (group 1) sit one of each per SIMD, and
     // run the same loop -- read a step's operands from LDS, barrier, run
     // its MFMAs, barrier -- with group 1 one phase behind (an extra barrier
@@ -456,9 +460,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     if (g1) {
       gemm_barrier();
     }
-    // The stages being read, kept as counters (A: ks % 2, B: ks % 3; bn:
-    // the B stage of step ks + 2).
-    uint32_t st = 0, sb = 0, bn = 2;
+    // The stages being read, kept as counters (A: ks % ASTAGES, B: ks % 3;
+    // an: the A stage of step ks + AAHEAD, bn: the B stage of step ks + 2).
+    uint32_t st = 0, sb = 0, an = AAHEAD, bn = 2;
     char *const bstages = lds + C::ASTAGES * C::A_BYTES;
 #pragma clang loop unroll(disable)
     for (uint32_t ks = 0; ks < nk; ++ks) {
@@ -466,15 +470,16 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       // phase just ended), group 1 B for step ks + 2 (its stage held step
       // ks - 1, read by both groups before this phase); ks counts the
       // item's K part, k0 + ks is the absolute step.
-      if (!g1 && ks + 1 < nk) {
-        copy_a_to(k0 + ks + 1, lds + (st ^ 1u) * C::A_BYTES);
+      if (!g1 && ks + AAHEAD < nk) {
+        copy_a_to(k0 + ks + AAHEAD, lds + an * C::A_BYTES);
       }
       if (g1 && ks + 2 < nk) {
         copy_b_to(k0 + ks + 2, bstages + bn * C::B_BYTES);
       }
       const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
       const char *Bs = bstages + sb * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
-      st ^= 1u;
+      st = st == C::ASTAGES - 1 ? 0u : st + 1u;
+      an = an == C::ASTAGES - 1 ? 0u : an + 1u;
       sb = sb == 2 ? 0u : sb + 1u;
       bn = bn == 2 ? 0u : bn + 1u;
 #pragma unroll
@@ -507,7 +512,13 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       if (!g1) {
-        __builtin_amdgcn_s_waitcnt(0);  // step ks + 1's A copies have landed
+        // Step ks + 1's A copies have landed; with three A stages step
+        // ks + 2's stay in flight.
+        if (AAHEAD == 2 && ks + 2 < nk) {
+          wait_vm<C::A_COPIES>();
+        } else {
+          __builtin_amdgcn_s_waitcnt(0);
+        }
       }
       gemm_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -659,8 +670,8 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   const uint32_t next = id + gridDim.x;
   const bool more = next < total;
   // The epilogue leaves the stages of the next tile's first copies alone
-  // (its LDS chunks lie past the stages, or in A stage 1 with three B
-  // stages), so those copies are issued during it: after the scales below
+  // (its LDS chunks lie past the stages, or in the last A stage in the
+  // ping-pong blocks), so those copies are issued during it: after the scales below
   // are in use (waiting for them then does not wait for the copies) and
   // before the stores.
   auto issue_next = [&]() {
@@ -873,11 +884,16 @@ using GemmNarrow192 = GemmCfg<256, 192, 4, 2, 3, 2, true>;
 // and needs more than the 128 registers per wave two workgroups allow.
 using GemmMid = GemmCfg<128, 128, 2, 4>;
 // 128 columns: 4 waves of 64 rows x 2 of 64 columns, ping-pong with three B
-// stages, one workgroup per CU, for N = 4096-class grids (one full round of
-// 256 x 128 tiles at M = 2048).
-using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 2, true>;
-// 64 columns: 4 waves of 64 rows x 2 of 32 columns, for the smallest grids.
-using GemmNarrow64 = GemmCfg<256, 64, 4, 2, 3, 2, true>;
+// and three A stages (144 KiB), one workgroup per CU, for N = 4096-class
+// grids (one full round of 256 x 128 tiles at M = 2048).
+using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 3, true>;
+// 64 columns: 4 waves of 64 rows x 2 of 32 columns, for the smallest grids;
+// three B and three A stages (120 KiB).  With A copied two k-steps ahead
+// instead of one (both widths; MI355X, K = 4096 unless noted): M=120
+// N=14336 24.0 against 26.9 us, M=768 N=4096 23.3 against 25.5, M=256
+// N=14336 27.1 against 29.9, M=512 N=4096 K=14336 48.2 against 51.5, M=256
+// N=4096 18.7 against 19.5; M=2048 N=4096 level.
+using GemmNarrow64 = GemmCfg<256, 64, 4, 2, 3, 3, true>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
