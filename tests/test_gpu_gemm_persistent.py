@@ -33,16 +33,19 @@ PERSISTENT = [
     ("256x192", 250, 98304, 256),    # 512 tiles
     ("128x128", 1100, 14000, 256),   # 990 tiles on 512 workgroups, ragged N
 ]
-# One round of 256-row ping-pong blocks (the N = 4096 and 6144 prefill
-# shapes, and a 256-column one) with several k-steps, so the three-stage B
-# ring wraps: the launch is not persistent, so only the block is asserted.
+# One round of ping-pong blocks (the N = 4096 and 6144 prefill shapes, a
+# 256-column one, and the 128 x 64 and 64 x 64 blocks of short prompts) with
+# several k-steps, so the three-stage rings wrap: the launch is not
+# persistent, so only the block is asserted.
 ONE_ROUND = [
     ("256x128", 2048, 4096, 256),    # 256 tiles on 256 CUs
     ("256x64", 1024, 4000, 128),     # 252 tiles, ragged N
     ("256x256", 2048, 8192, 512),    # 256 tiles, four k-steps
     ("256x192", 2048, 6144, 384),    # 256 tiles, three k-steps
-    ("256x64", 256, 4096, 512),      # 64 tiles, the smallest grids
-    ("256x64", 300, 2000, 256),      # 64 tiles, ragged M and N
+    ("64x64", 256, 4096, 512),       # 256 tiles of the short-prompt blocks
+    ("64x64", 300, 2000, 256),       # 160 tiles, ragged M and N
+    ("128x64", 120, 14336, 512),     # 224 tiles, one ragged 128-row block
+    ("128x64", 100, 6000, 4096),     # 94 tiles, K split in two
 ]
 CASES = [c + (True,) for c in PERSISTENT] + [c + (False,) for c in ONE_ROUND]
 

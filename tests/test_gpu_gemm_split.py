@@ -23,14 +23,18 @@ pytestmark = pytest.mark.gpu
 
 # (M, N, K, K parts expected on a 256-CU device)
 SPLIT = [
-    (256, 4096, 4096, 2),    # 64 tiles of 256 x 64, 16 k-steps per part
-    (300, 2000, 4096, 2),    # ragged M and N
+    (256, 4096, 4096, 2),    # 128 tiles of 128 x 64, 16 k-steps per part
+    (300, 2000, 4096, 2),    # ragged M and N (128 x 64)
     (300, 2000, 4224, 2),    # 33 k-steps: parts of 17 and 16
-    (256, 1024, 8320, 4),    # 65 k-steps: parts of 17, 17, 17 and 14
-    (256, 256, 4096, 2),     # 4 tiles
-    (256, 4480, 6144, 3),    # 70 tiles, 48 k-steps: three parts of 16
-    (256, 2048, 14336, 7),   # 32 tiles, 112 k-steps: seven parts of 16
-    (256, 2048, 14208, 6),   # 111 k-steps: five parts of 19 and one of 16
+    (256, 1024, 8320, 4),    # 64 x 64; 65 k-steps: parts of 17, 17, 17, 14
+    (256, 256, 4096, 2),     # 16 tiles of 64 x 64
+    (256, 4480, 6144, 3),    # 70 tiles of 256 x 64, 48 k-steps: three of 16
+    (256, 2304, 14336, 7),   # 36 tiles of 256 x 64: seven parts of 16
+    (64, 2048, 14336, 7),    # 32 tiles of 64 x 64: seven parts of 16
+    (256, 2048, 14208, 4),   # 128 x 64; 111 k-steps: three of 28, one of 27
+    (256, 2560, 14208, 6),   # 256 x 64; five parts of 19 and one of 16
+    (64, 2560, 14208, 6),    # the same split on 64 x 64 blocks
+    (16, 4096, 4096, 2),     # M below one MFMA tile
 ]
 
 
@@ -154,7 +158,8 @@ def test_split_plan_invariants(uh, gpu):
                 seen.add(p.split_k)
                 kpp = -(-steps // p.split_k)
                 assert p.kernel == uh.KERNEL_GEMM_LDS
-                assert p.block_m == 256, (m, n, k, p.block_m)
+                assert p.block_m in (64, 128, 256) and p.block_n == 64 or \
+                    p.block_m == 256, (m, n, k, p.block_m, p.block_n)
                 assert kpp >= 16 and (p.split_k - 1) * kpp < steps, (m, n, k, p.split_k)
                 assert p.grid == p.tiles * p.split_k <= cus, (m, n, k, p.grid)
                 assert p.tiles * 4 <= 1024

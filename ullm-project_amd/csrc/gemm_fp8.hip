@@ -166,8 +166,10 @@ struct GemmCfg {
   // and 256 x 64 blocks, whose grids of at most a few rounds leave each CU
   // waiting on its copies (below).
   static constexpr uint32_t ASTAGES = ASTAGES_;
-  static_assert(ASTAGES >= 2 && ASTAGES <= 3 && BSTAGES >= 2 && BSTAGES <= 3,
-                "one or two k-steps of look-ahead");
+  // Look-ahead of one or two k-steps, up to three in the ping-pong loop.
+  static_assert(ASTAGES >= 2 && BSTAGES >= 2 && ASTAGES <= (PP ? 4 : 3) &&
+                    BSTAGES <= (PP ? 4 : 3),
+                "k-steps of look-ahead");
   static constexpr uint32_t WAVES = WM * WN;
   static constexpr uint32_t TM = BM / WM / 16;  // 16-row m-tiles per wave
   static constexpr uint32_t TN = BN / WN / 16;  // 16-column n-tiles per wave
@@ -198,7 +200,7 @@ struct GemmCfg {
   // copies leave alone.
   // With a third A stage (A copied two k-steps ahead too) the chunks move
   // to A stage 2: the next tile's first copies fill A stages 0 and 1.
-  static_assert(!PP || BSTAGES == 3, "ping-pong: three B stages");
+  static_assert(!PP || BSTAGES >= 3, "ping-pong: at least three B stages");
   static constexpr uint32_t CHUNK_BASE = PP ? (ASTAGES - 1) * A_BYTES : STAGE_BYTES;
   static_assert(!PP || WAVES * CHUNK_BYTES <= A_BYTES,
                 "epilogue chunks fit the last A stage");
@@ -460,9 +462,9 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     if (g1) {
       gemm_barrier();
     }
-    // The stages being read, kept as counters (A: ks % ASTAGES, B: ks % 3;
-    // an: the A stage of step ks + AAHEAD, bn: the B stage of step ks + 2).
-    uint32_t st = 0, sb = 0, an = AAHEAD, bn = 2;
+    // The stages being read, kept as counters (A: ks % ASTAGES, B:
+    // ks % BSTAGES; an, bn: the stages of steps ks + AAHEAD, ks + BAHEAD).
+    uint32_t st = 0, sb = 0, an = AAHEAD, bn = BAHEAD;
     char *const bstages = lds + C::ASTAGES * C::A_BYTES;
 #pragma clang loop unroll(disable)
     for (uint32_t ks = 0; ks < nk; ++ks) {
@@ -473,15 +475,15 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       if (!g1 && ks + AAHEAD < nk) {
         copy_a_to(k0 + ks + AAHEAD, lds + an * C::A_BYTES);
       }
-      if (g1 && ks + 2 < nk) {
-        copy_b_to(k0 + ks + 2, bstages + bn * C::B_BYTES);
+      if (g1 && ks + BAHEAD < nk) {
+        copy_b_to(k0 + ks + BAHEAD, bstages + bn * C::B_BYTES);
       }
       const char *As = lds + st * C::A_BYTES + (wm * C::TM * 16 + lane % 16) * 128;
       const char *Bs = bstages + sb * C::B_BYTES + (wn * C::TN * 2) * 1024 + lane * 16;
       st = st == C::ASTAGES - 1 ? 0u : st + 1u;
       an = an == C::ASTAGES - 1 ? 0u : an + 1u;
-      sb = sb == 2 ? 0u : sb + 1u;
-      bn = bn == 2 ? 0u : bn + 1u;
+      sb = sb == C::BSTAGES - 1 ? 0u : sb + 1u;
+      bn = bn == C::BSTAGES - 1 ? 0u : bn + 1u;
 #pragma unroll
       for (uint32_t i = 0; i < C::TM; ++i) {
         af[i] = a_operand(As, i);
@@ -490,12 +492,13 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       for (uint32_t j = 0; j < C::TN; ++j) {
         bf[j] = lds_operand(Bs + j * 2048);
       }
-      // Group 1: step ks + 1's B copies (issued a step ago) have landed
-      // before the barrier after which group 0 reads them; step ks + 2's
-      // stay in flight.
+      // Group 1: step ks + 1's B copies have landed before the barrier
+      // after which group 0 reads them; those of the later steps stay in
+      // flight (near the end of the part, when fewer were issued, wait for
+      // all).
       if (g1) {
-        if (ks + 2 < nk) {
-          wait_vm<C::B_COPIES>();
+        if (ks + BAHEAD < nk) {
+          wait_vm<(BAHEAD - 1) * C::B_COPIES>();
         } else {
           __builtin_amdgcn_s_waitcnt(0);
         }
@@ -512,10 +515,10 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       __builtin_amdgcn_sched_barrier(0);
       if (!g1) {
-        // Step ks + 1's A copies have landed; with three A stages step
-        // ks + 2's stay in flight.
-        if (AAHEAD == 2 && ks + 2 < nk) {
-          wait_vm<C::A_COPIES>();
+        // Step ks + 1's A copies have landed; with more A stages those of
+        // the later steps stay in flight.
+        if (AAHEAD > 1 && ks + AAHEAD < nk) {
+          wait_vm<(AAHEAD - 1) * C::A_COPIES>();
         } else {
           __builtin_amdgcn_s_waitcnt(0);
         }
@@ -620,10 +623,10 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
       }
       __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores completed
       gemm_barrier();
-      // The flag lives in B stage 2, which no copy targets until the next
+      // The flag lives in the last B stage, which no copy targets until the next
       // item's prologue (issued below, after the flag is read).
       uint32_t *flag = reinterpret_cast<uint32_t *>(lds + C::ASTAGES * C::A_BYTES +
-                                                    2 * C::B_BYTES);
+                                                    (C::BSTAGES - 1) * C::B_BYTES);
       if (threadIdx.x == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(a.cnt + ctile, 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -894,6 +897,11 @@ using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 3, true>;
 // N=14336 27.1 against 29.9, M=512 N=4096 K=14336 48.2 against 51.5, M=256
 // N=4096 18.7 against 19.5; M=2048 N=4096 level.
 using GemmNarrow64 = GemmCfg<256, 64, 4, 2, 3, 3, true>;
+// 128 and 64 rows by 64 columns for short prompts (block_m_64): 4 x 2 waves
+// of 32 x 32 and 2 x 4 waves of 32 x 16, ping-pong, three A and three B
+// stages (72 and 48 KiB).
+using GemmSmall128 = GemmCfg<128, 64, 4, 2, 3, 3, true>;
+using GemmSmall64 = GemmCfg<64, 64, 2, 4, 3, 3, true>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
@@ -966,16 +974,16 @@ bool gemm_use_64(uint32_t m, uint32_t n, uint32_t cus) {
 }
 
 // Split K over workgroups on grids of few tiles (ping-pong blocks, one round,
-// at most half of the CUs busy): a 256-row tile's k-loop takes ~0.7 us per
-// 128-deep step however little each step holds, so the idle CUs take parts
-// of K, at least 16 steps each, and the last part of a tile to finish adds
-// the parts.  ULLM_GEMM_SPLIT=0 (read only by a -DULLM_TUNING build) turns
-// it off.
-void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
-  p.ksplit = 1;
+// at most half of the CUs busy): a tile's k-loop then runs at the copy rate
+// of one CU however many CUs idle, so the idle CUs take parts of K, at
+// least 16 steps each, and the last part of a tile to finish adds the parts.
+// K parts for `tiles` one-workgroup tiles of bm x bn (1: no split).
+// ULLM_GEMM_SPLIT=0 (read only by a -DULLM_TUNING build) turns it off.
+uint32_t split_parts(uint32_t tiles, uint32_t k, uint32_t cus, uint32_t bm,
+                     uint32_t bn) {
   const char *env = tuning_env("ULLM_GEMM_SPLIT");
-  if ((env != nullptr && env[0] == '0') || p.grid < p.tiles) {
-    return;
+  if (env != nullptr && env[0] == '0') {
+    return 1;
   }
   // A part of fewer than 16 k-steps does not pay for its partial-sum round
   // trip (store, counter, reload by the finisher): with 8 the measured
@@ -985,21 +993,72 @@ void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
     min_steps = std::max(1, std::atoi(v));
   }
   const uint32_t ksteps = k / 128;
-  if (ksteps < 2 * min_steps || 2 * p.tiles > cus ||
-      p.tiles * 4 > kGemmCounterBytes) {
-    return;
+  if (ksteps < 2 * min_steps || 2 * tiles > cus || tiles * 4 > kGemmCounterBytes) {
+    return 1;
   }
-  uint32_t ks = std::min(cus / p.tiles, ksteps / min_steps);
+  uint32_t ks = std::min(cus / tiles, ksteps / min_steps);
   // Every part holds at least one step.
   while (ks > 1 && (ks - 1) * ((ksteps + ks - 1) / ks) >= ksteps) {
     --ks;
   }
-  const uint64_t part = uint64_t(p.tiles) * ks * p.block_m * p.block_n * 4;
-  if (ks < 2 || part >= (uint64_t(1) << 31)) {
-    return;
+  const uint64_t part = uint64_t(tiles) * ks * bm * bn * 4;
+  return ks < 2 || part >= (uint64_t(1) << 31) ? 1 : ks;
+}
+
+void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
+  p.ksplit = 1;
+  if (p.grid < p.tiles) {
+    return;  // persistent: every CU already busy
   }
-  p.ksplit = ks;
-  p.grid = p.tiles * ks;
+  const uint32_t ks = split_parts(p.tiles, k, cus, p.block_m, p.block_n);
+  if (ks > 1) {
+    p.ksplit = ks;
+    p.grid = p.tiles * ks;
+  }
+}
+
+// Rows of the 64-column blocks (256, 128 or 64).  On the grids these blocks
+// serve (one round or a few) a workgroup's k-loop runs at the rate one CU
+// copies its operands into LDS, ~60 GB/s per CU whatever the block's MFMA
+// work: a k-step of a 256 x 64 block (40 KiB) took ~0.67 us, of a 128 x 64
+// block (24 KiB) ~0.41 us, of a 64 x 64 block (16 KiB) ~0.27 us (MI355X,
+// every CU busy).  So the launch takes about rounds x k-steps per
+// workgroup x bytes per k-step, with rows past M costing nothing (they
+// repeat the last row, an L2 hit), plus, with K split, the partial sums'
+// round trip (in proportion to the block's rows); the fewest rows win ties
+// (less MFMA work, fewer padded rows).  The 128- and 64-row blocks are
+// taken on one round only: over several rounds they lost every time.
+// Measured (K = 4096 unless noted; 256 / 128 / 64 rows): M=64 N=4096 18.0 /
+// 13.9 / 12.5 us, M=256 N=4096 18.7 / 14.6 / 16.8, M=256 N=6144 20.0 / 18.5
+// / 20.5, M=120 N=14336 23.9 / 20.4 / 22.8, M=256 N=2048 K=14208 33.0 /
+// 23.4 / -, M=256 N=14336 26.7 / 28.9 / 39.9, M=512 N=4096 K=14336 47.5 /
+// 55.5 / 64.0, M=768 N=4096 23.3 / 24.6 / 32.6, M=300 N=6000 22.7 / 25.1 /
+// 24.3: the model picks the fastest of each.
+uint32_t block_m_64(uint32_t m, uint32_t n, uint32_t k, uint32_t cus) {
+  if (const char *v = tuning_env("ULLM_GEMM_BM")) {
+    const int bm = std::atoi(v);
+    if (bm == 64 || bm == 128 || bm == 256) {
+      return uint32_t(bm);
+    }
+  }
+  const uint64_t ksteps = k / 128;
+  uint32_t best = 256;
+  uint64_t best_cost = ~uint64_t(0);
+  for (uint32_t bm : {64u, 128u, 256u}) {
+    const uint32_t tiles = ((m + bm - 1) / bm) * ((n + 63) / 64);
+    if (bm < 256 && tiles > cus) {
+      continue;
+    }
+    const uint32_t ks = split_parts(tiles, k, cus, bm, 64);
+    const uint64_t rounds = (uint64_t(tiles) * ks + cus - 1) / cus;
+    const uint64_t steps = (ksteps + ks - 1) / ks;
+    const uint64_t cost = rounds * steps * (std::min(bm, m) + 64) + (ks > 1 ? 6 * bm : 0);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = bm;
+    }
+  }
+  return best;
 }
 
 template <class C>
@@ -1065,6 +1124,8 @@ hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
     case kGemmNarrow192: return launch_gemm_lds<GemmNarrow192, EPI>(a, p, s);
     case kGemmNarrow128: return launch_gemm_lds<GemmNarrow128, EPI>(a, p, s);
     case kGemmNarrow64: return launch_gemm_lds<GemmNarrow64, EPI>(a, p, s);
+    case kGemmSmall128: return launch_gemm_lds<GemmSmall128, EPI>(a, p, s);
+    case kGemmSmall64: return launch_gemm_lds<GemmSmall64, EPI>(a, p, s);
     case kGemmLarge: return launch_gemm_lds<GemmLarge, EPI>(a, p, s);
     default: break;
   }
@@ -1102,8 +1163,11 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
   const bool narrow = forced_bn == 0 && cfg == nullptr && gemm_use_mid(m, n, cus) &&
                       gemm_use_128(m, n, cus);
   if (forced_bn == 64 || (narrow && gemm_use_64(m, n, cus))) {
-    p.kind = kGemmNarrow64;
-    fill_plan<GemmNarrow64>(p, m, n, cus, persist);
+    switch (block_m_64(m, n, k, cus)) {
+      case 64: p.kind = kGemmSmall64; fill_plan<GemmSmall64>(p, m, n, cus, persist); break;
+      case 128: p.kind = kGemmSmall128; fill_plan<GemmSmall128>(p, m, n, cus, persist); break;
+      default: p.kind = kGemmNarrow64; fill_plan<GemmNarrow64>(p, m, n, cus, persist); break;
+    }
     plan_split(p, k, cus);
     return p;
   }

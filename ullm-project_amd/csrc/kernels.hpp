@@ -93,6 +93,8 @@ enum GemmKind : uint32_t {
   kGemmMid = 4,         // LDS-pipelined 128 x 128, two workgroups per CU
   kGemmNarrow128 = 5,   // LDS-pipelined 256 x 128
   kGemmNarrow64 = 6,    // LDS-pipelined 256 x 64
+  kGemmSmall128 = 7,    // LDS-pipelined 128 x 64 (short prompts)
+  kGemmSmall64 = 8,     // LDS-pipelined 64 x 64 (short prompts)
 };
 struct GemmPlan {
   uint32_t kind, block_m, block_n, tiles, grid;
