@@ -46,6 +46,8 @@ ONE_ROUND = [
     ("64x64", 300, 2000, 256),       # 160 tiles, ragged M and N
     ("128x64", 120, 14336, 512),     # 224 tiles, one ragged 128-row block
     ("128x64", 100, 6000, 4096),     # 94 tiles, K split in two
+    ("64x128", 40, 28672, 512),      # 224 tiles, chunks past the stages
+    ("128x128", 128, 28672, 384),    # 224 tiles of the 128-column short blocks
 ]
 CASES = [c + (True,) for c in PERSISTENT] + [c + (False,) for c in ONE_ROUND]
 

@@ -200,14 +200,16 @@ struct GemmCfg {
   // copies leave alone.
   // With a third A stage (A copied two k-steps ahead too) the chunks move
   // to A stage 2: the next tile's first copies fill A stages 0 and 1.
+  // Blocks whose A stage is too small for them keep the chunks past the
+  // stages.
   static_assert(!PP || BSTAGES >= 3, "ping-pong: at least three B stages");
-  static constexpr uint32_t CHUNK_BASE = PP ? (ASTAGES - 1) * A_BYTES : STAGE_BYTES;
-  static_assert(!PP || WAVES * CHUNK_BYTES <= A_BYTES,
-                "epilogue chunks fit the last A stage");
+  static constexpr bool CHUNKS_IN_A = PP && WAVES * CHUNK_BYTES <= A_BYTES;
+  static constexpr uint32_t CHUNK_BASE =
+      CHUNKS_IN_A ? (ASTAGES - 1) * A_BYTES : STAGE_BYTES;
   // The ping-pong loop waits for a step's B copies by count (each copying
   // wave issues B_COPIES per step), so every copying wave must issue as many.
   static_assert(!PP || B_TILES % CW == 0, "B copies split evenly");
-  static constexpr uint32_t LDS = PP ? STAGE_BYTES : STAGE_BYTES + WAVES * CHUNK_BYTES;
+  static constexpr uint32_t LDS = STAGE_BYTES + (CHUNKS_IN_A ? 0 : WAVES * CHUNK_BYTES);
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
 
@@ -897,11 +899,14 @@ using GemmNarrow128 = GemmCfg<256, 128, 4, 2, 3, 3, true>;
 // N=14336 27.1 against 29.9, M=512 N=4096 K=14336 48.2 against 51.5, M=256
 // N=4096 18.7 against 19.5; M=2048 N=4096 level.
 using GemmNarrow64 = GemmCfg<256, 64, 4, 2, 3, 3, true>;
-// 128 and 64 rows by 64 columns for short prompts (block_m_64): 4 x 2 waves
-// of 32 x 32 and 2 x 4 waves of 32 x 16, ping-pong, three A and three B
-// stages (72 and 48 KiB).
+// 128 and 64 rows by 64 or 128 columns for short prompts (block_m_for):
+// ping-pong, three A and three B stages; waves of 32 x 32 (128 x 64, 4 x 2
+// waves), 32 x 16 (64 x 64, 2 x 4), 64 x 32 (128 x 128, 2 x 4) and 32 x 32
+// (64 x 128, 2 x 4; its epilogue chunks lie past the stages).
 using GemmSmall128 = GemmCfg<128, 64, 4, 2, 3, 3, true>;
 using GemmSmall64 = GemmCfg<64, 64, 2, 4, 3, 3, true>;
+using GemmSmall128W = GemmCfg<128, 128, 2, 4, 3, 3, true>;
+using GemmSmall64W = GemmCfg<64, 128, 2, 4, 3, 3, true>;
 
 
 // Block width (256, 224 or 192 columns, 256 rows) whose rounds of
@@ -1017,7 +1022,7 @@ void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
   }
 }
 
-// Rows of the 64-column blocks (256, 128 or 64).  On the grids these blocks
+// Rows of the 64- or 128-column blocks (256, 128 or 64).  On the grids these blocks
 // serve (one round or a few) a workgroup's k-loop runs at the rate one CU
 // copies its operands into LDS, ~60 GB/s per CU whatever the block's MFMA
 // work: a k-step of a 256 x 64 block (40 KiB) took ~0.67 us, of a 128 x 64
@@ -1034,7 +1039,7 @@ void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
 // 23.4 / -, M=256 N=14336 26.7 / 28.9 / 39.9, M=512 N=4096 K=14336 47.5 /
 // 55.5 / 64.0, M=768 N=4096 23.3 / 24.6 / 32.6, M=300 N=6000 22.7 / 25.1 /
 // 24.3: the model picks the fastest of each.
-uint32_t block_m_64(uint32_t m, uint32_t n, uint32_t k, uint32_t cus) {
+uint32_t block_m_for(uint32_t bn, uint32_t m, uint32_t n, uint32_t k, uint32_t cus) {
   if (const char *v = tuning_env("ULLM_GEMM_BM")) {
     const int bm = std::atoi(v);
     if (bm == 64 || bm == 128 || bm == 256) {
@@ -1045,14 +1050,14 @@ uint32_t block_m_64(uint32_t m, uint32_t n, uint32_t k, uint32_t cus) {
   uint32_t best = 256;
   uint64_t best_cost = ~uint64_t(0);
   for (uint32_t bm : {64u, 128u, 256u}) {
-    const uint32_t tiles = ((m + bm - 1) / bm) * ((n + 63) / 64);
+    const uint32_t tiles = ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
     if (bm < 256 && tiles > cus) {
       continue;
     }
-    const uint32_t ks = split_parts(tiles, k, cus, bm, 64);
+    const uint32_t ks = split_parts(tiles, k, cus, bm, bn);
     const uint64_t rounds = (uint64_t(tiles) * ks + cus - 1) / cus;
     const uint64_t steps = (ksteps + ks - 1) / ks;
-    const uint64_t cost = rounds * steps * (std::min(bm, m) + 64) + (ks > 1 ? 6 * bm : 0);
+    const uint64_t cost = rounds * steps * (std::min(bm, m) + bn) + (ks > 1 ? 6 * bm : 0);
     if (cost < best_cost) {
       best_cost = cost;
       best = bm;
@@ -1126,6 +1131,8 @@ hipError_t gemm_e(const GemmArgs &a, const GemmPlan &p, bool vec,
     case kGemmNarrow64: return launch_gemm_lds<GemmNarrow64, EPI>(a, p, s);
     case kGemmSmall128: return launch_gemm_lds<GemmSmall128, EPI>(a, p, s);
     case kGemmSmall64: return launch_gemm_lds<GemmSmall64, EPI>(a, p, s);
+    case kGemmSmall128W: return launch_gemm_lds<GemmSmall128W, EPI>(a, p, s);
+    case kGemmSmall64W: return launch_gemm_lds<GemmSmall64W, EPI>(a, p, s);
     case kGemmLarge: return launch_gemm_lds<GemmLarge, EPI>(a, p, s);
     default: break;
   }
@@ -1163,7 +1170,7 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
   const bool narrow = forced_bn == 0 && cfg == nullptr && gemm_use_mid(m, n, cus) &&
                       gemm_use_128(m, n, cus);
   if (forced_bn == 64 || (narrow && gemm_use_64(m, n, cus))) {
-    switch (block_m_64(m, n, k, cus)) {
+    switch (block_m_for(64, m, n, k, cus)) {
       case 64: p.kind = kGemmSmall64; fill_plan<GemmSmall64>(p, m, n, cus, persist); break;
       case 128: p.kind = kGemmSmall128; fill_plan<GemmSmall128>(p, m, n, cus, persist); break;
       default: p.kind = kGemmNarrow64; fill_plan<GemmNarrow64>(p, m, n, cus, persist); break;
@@ -1172,8 +1179,11 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
     return p;
   }
   if (forced_bn == 128 || narrow) {
-    p.kind = kGemmNarrow128;
-    fill_plan<GemmNarrow128>(p, m, n, cus, persist);
+    switch (block_m_for(128, m, n, k, cus)) {
+      case 64: p.kind = kGemmSmall64W; fill_plan<GemmSmall64W>(p, m, n, cus, persist); break;
+      case 128: p.kind = kGemmSmall128W; fill_plan<GemmSmall128W>(p, m, n, cus, persist); break;
+      default: p.kind = kGemmNarrow128; fill_plan<GemmNarrow128>(p, m, n, cus, persist); break;
+    }
     plan_split(p, k, cus);
     return p;
   }

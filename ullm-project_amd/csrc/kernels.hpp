@@ -95,6 +95,8 @@ enum GemmKind : uint32_t {
   kGemmNarrow64 = 6,    // LDS-pipelined 256 x 64
   kGemmSmall128 = 7,    // LDS-pipelined 128 x 64 (short prompts)
   kGemmSmall64 = 8,     // LDS-pipelined 64 x 64 (short prompts)
+  kGemmSmall128W = 9,   // LDS-pipelined 128 x 128 (short prompts)
+  kGemmSmall64W = 10,   // LDS-pipelined 64 x 128 (short prompts)
 };
 struct GemmPlan {
   uint32_t kind, block_m, block_n, tiles, grid;
