@@ -214,7 +214,9 @@ struct GemmCfg {
   // the tile's start, under its first copies, instead of after the k-loop
   // (MI355X: M=64 N=4096 K=4096 11.9 against 12.5 us, M=256 N=6144 18.0
   // against 18.5, M=64 N=28672 26.1-26.3 against 26.8-27.0).  The wide
-  // blocks keep the late gather: their k-loop has no registers to spare.
+  // blocks keep the late gather: early, it measured level on the 224-, 192-
+  // and 128-column blocks and slowed the 256 x 256 one from 55 to 101 us
+  // (M=2048 N=8192).
   static constexpr bool EARLY_SCALES = PP && BM < 256;
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
