@@ -304,9 +304,15 @@ __device__ __forceinline__ u32x2 pack_bf16x4(f32x4 t) {
   return u32x2{f32x2_to_bf16x2(t[0], t[1]), f32x2_to_bf16x2(t[2], t[3])};
 }
 
-template <class C, uint32_t EPI>
+// SPLIT: the launch splits K (a.ksplit > 1, ping-pong blocks only).  A
+// separate instantiation keeps the split's bookkeeping out of every other
+// launch: compiled into the persistent 256 x 224 kernel as a runtime branch
+// it cost 7-8 % (M=2048 N=28672 K=4096 214-216 against 199-201 us, M=4096
+// N=14336 209-211 against 192-194 on one MI355X).
+template <class C, uint32_t EPI, bool SPLIT>
 __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     GemmArgs a) {
+  static_assert(!SPLIT || C::PP, "K split: ping-pong blocks only");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   // sharing one L2 also share operand tiles, and with a grid that is a
   // multiple of 8 every id of one workgroup stays on its XCD.
   // Work items: (tile, K part); without a split one per tile.
-  const uint32_t ksplit = C::PP ? a.ksplit : 1u;
+  const uint32_t ksplit = SPLIT ? a.ksplit : 1u;
   const uint32_t total = mblocks * nblocks * ksplit;
   const uint32_t stripes = (a.n + 15) / 16;
   const uint32_t ksteps = a.k / C::BK;
@@ -625,8 +631,8 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
   }
 
   // The main loop ended on a barrier: every operand stage is free.
-  if constexpr (C::PP) {
-    if (ksplit > 1) {
+  if constexpr (SPLIT) {
+    {
       // Split K: every part stores its fp32 sums; the last part of the tile
       // to arrive adds all parts in part order (the result does not depend
       // on the arrival order) and runs the epilogue, the others move on.
@@ -1129,12 +1135,24 @@ hipError_t raise_lds_limit(const void *kernel, uint32_t bytes) {
 template <class C, uint32_t EPI>
 hipError_t launch_gemm_lds(const GemmArgs &a, const GemmPlan &p,
                            hipStream_t s) {
-  const void *k = reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI>);
+  if constexpr (C::PP) {
+    if (p.ksplit > 1) {
+      const void *ks = reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI, true>);
+      const hipError_t attr = raise_lds_limit(ks, C::LDS);
+      if (attr != hipSuccess) {
+        return attr;
+      }
+      hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI, true>), dim3(p.grid),
+                         dim3(C::WAVES * kWave), C::LDS, s, a);
+      return hipGetLastError();
+    }
+  }
+  const void *k = reinterpret_cast<const void *>(fp8_gemm_lds_kernel<C, EPI, false>);
   const hipError_t attr = raise_lds_limit(k, C::LDS);
   if (attr != hipSuccess) {
     return attr;
   }
-  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI>), dim3(p.grid),
+  hipLaunchKernelGGL((fp8_gemm_lds_kernel<C, EPI, false>), dim3(p.grid),
                      dim3(C::WAVES * kWave), C::LDS, s, a);
   return hipGetLastError();
 }
