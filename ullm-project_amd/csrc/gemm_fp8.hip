@@ -1198,7 +1198,9 @@ GemmPlan plan_fp8_gemm(uint32_t m, uint32_t n, uint32_t k, bool vec,
     return p;
   }
   // Tuning overrides (read only by a -DULLM_TUNING build): ULLM_GEMM_CFG=mid,
-  // ULLM_GEMM_BN=256/224/192, ULLM_GEMM_PERSIST=0 (one workgroup per tile).
+  // ULLM_GEMM_BN=256/224/192/128/64, ULLM_GEMM_BM=256/128/64 (rows of the 64-
+  // and 128-column blocks), ULLM_GEMM_PERSIST=0 (one workgroup per tile),
+  // ULLM_GEMM_SPLIT=0 and ULLM_GEMM_SPLIT_STEPS (the K split).
   const char *cfg = tuning_env("ULLM_GEMM_CFG");
   const char *bn_env = tuning_env("ULLM_GEMM_BN");
   const char *persist_env = tuning_env("ULLM_GEMM_PERSIST");
