@@ -483,11 +483,13 @@ __global__ __launch_bounds__(C::WAVES *kWave) void fp8_gemm_lds_kernel(
     // its MFMAs, barrier -- with group 1 one phase behind (an extra barrier
     // before its loop, matched by one after group 0's).  While one wave of
     // a SIMD waits on LDS the other keeps the matrix core busy.  Group 0
-    // issues the A copies for step ks + 1 before it reads step ks (their
-    // stage was last read by group 1 in the phase just ended) and waits for
-    // them before the barrier that ends its MFMA phase; group 1 issues the
-    // B copies for step ks + 2 (three B stages) before it reads step ks and
+    // issues the A copies for step ks + AAHEAD (ASTAGES - 1 steps ahead:
+    // their stage was last read by group 1 in the phase just ended) before
+    // it reads step ks, and waits for step ks + 1's before the barrier that
+    // ends its MFMA phase; group 1 issues the B copies for step ks + BAHEAD
+    // (two steps ahead with three B stages) before it reads step ks and
     // waits for step ks + 1's before the barrier that ends its read phase.
+    // Waits count copies, so the later steps' stay in flight.
     // Each phase then carries about half of a step's copy instructions.
     // The copies slow the loop in proportion to the instructions issued in
     // one phase, not by their latency (waiting for them costs ~1 %): on
