@@ -1,6 +1,7 @@
 """GPU parity of the prefill FP8 GEMM when it splits K over workgroups.
 
-Grids of few output tiles (at most half of the CUs busy, K >= 4096) run each
+Grids of few output tiles (at most half of the CUs busy, K of at least 32
+k-steps of 128, 16 in 64 x 64 blocks) run each
 tile's K in parts on otherwise idle CUs; the last part of a tile to finish
 adds the fp32 partial sums in part order and runs the epilogue.  Checked
 against the oracle on sampled rows (rows of a GEMM are independent), for each
@@ -27,14 +28,14 @@ SPLIT = [
     (300, 2000, 4096, 2),    # ragged M and N (128 x 64)
     (300, 2000, 4224, 2),    # 33 k-steps: parts of 17 and 16
     (256, 1024, 8320, 4),    # 64 x 64; 65 k-steps: parts of 17, 17, 17, 14
-    (256, 256, 4096, 2),     # 16 tiles of 64 x 64
+    (256, 256, 4096, 4),     # 16 tiles of 64 x 64: four parts of 8
     (256, 4480, 6144, 3),    # 70 tiles of 256 x 64, 48 k-steps: three of 16
-    (256, 2304, 14336, 7),   # 36 tiles of 256 x 64: seven parts of 16
-    (64, 2048, 14336, 7),    # 32 tiles of 64 x 64: seven parts of 16
+    (256, 2304, 14336, 3),   # 72 tiles of 128 x 64: parts of 38, 38, 36
+    (64, 2048, 14336, 8),    # 32 tiles of 64 x 64: eight parts of 14
     (256, 2048, 14208, 4),   # 128 x 64; 111 k-steps: three of 28, one of 27
-    (256, 2560, 14208, 6),   # 256 x 64; five parts of 19 and one of 16
+    (256, 2560, 14208, 3),   # 80 tiles of 128 x 64; parts of 37, 37, 37
     (64, 2560, 14208, 6),    # the same split on 64 x 64 blocks
-    (16, 4096, 4096, 2),     # M below one MFMA tile
+    (16, 4096, 4096, 4),     # M below one MFMA tile
 ]
 
 
@@ -138,7 +139,7 @@ def test_split_gemm_caller_workspace(uh, orc, gpu):
 
 def test_split_plan_invariants(uh, gpu):
     """Every plan over a sweep of prefill shapes: a split has at least two
-    parts of at least 16 k-steps each (none empty), one workgroup per part,
+    parts of at least 16 k-steps each (8 in 64 x 64 blocks; none empty), one workgroup per part,
     at most one round of the CUs, counters within their 1 KiB region, and the
     workspace size that holds its partial sums."""
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
@@ -160,7 +161,8 @@ def test_split_plan_invariants(uh, gpu):
                 assert p.kernel == uh.KERNEL_GEMM_LDS
                 assert p.block_m in (64, 128, 256) and p.block_n == 64 or \
                     p.block_m == 256, (m, n, k, p.block_m, p.block_n)
-                assert kpp >= 16 and (p.split_k - 1) * kpp < steps, (m, n, k, p.split_k)
+                floor = 8 if p.block_m * p.block_n <= 64 * 64 else 16
+                assert kpp >= floor and (p.split_k - 1) * kpp < steps, (m, n, k, p.split_k)
                 assert p.grid == p.tiles * p.split_k <= cus, (m, n, k, p.grid)
                 assert p.tiles * 4 <= 1024
                 parts = p.tiles * p.split_k * p.block_m * p.block_n * 4

@@ -1020,7 +1020,9 @@ uint32_t split_parts(uint32_t tiles, uint32_t k, uint32_t cus, uint32_t bm,
   // A part of fewer than 16 k-steps does not pay for its partial-sum round
   // trip (store, counter, reload by the finisher): with 8 the measured
   // M=300 N=2000 K=2048 launch took 14.3 us split against 14.0 unsplit.
-  uint32_t min_steps = 16;
+  // The 64 x 64 blocks' partial sums are small enough for parts of 8
+  // (M=64 N=4096 K=4096 11.2 against 12.0 us, M=16 10.9 against 11.8).
+  uint32_t min_steps = bm * bn <= 64 * 64 ? 8 : 16;
   if (const char *v = tuning_env("ULLM_GEMM_SPLIT_STEPS")) {
     min_steps = std::max(1, std::atoi(v));
   }
@@ -1057,7 +1059,9 @@ void plan_split(GemmPlan &p, uint32_t k, uint32_t cus) {
 // every CU busy).  So the launch takes about rounds x k-steps per
 // workgroup x bytes per k-step, with rows past M costing nothing (they
 // repeat the last row, an L2 hit), plus, with K split, the partial sums'
-// round trip (in proportion to the block's rows); the fewest rows win ties
+// round trips (in proportion to the block's rows and the parts beyond the
+// first: 256-row blocks split 7 ways measured 33.0 against 23.4 us for
+// 128-row ones split 4 ways at M=256 N=2048 K=14336); the fewest rows win ties
 // (less MFMA work, fewer padded rows).  The 128- and 64-row blocks are
 // taken on one round only: over several rounds they lost every time.
 // Measured (K = 4096 unless noted; 256 / 128 / 64 rows): M=64 N=4096 18.0 /
@@ -1084,7 +1088,7 @@ uint32_t block_m_for(uint32_t bn, uint32_t m, uint32_t n, uint32_t k, uint32_t c
     const uint32_t ks = split_parts(tiles, k, cus, bm, bn);
     const uint64_t rounds = (uint64_t(tiles) * ks + cus - 1) / cus;
     const uint64_t steps = (ksteps + ks - 1) / ks;
-    const uint64_t cost = rounds * steps * (std::min(bm, m) + bn) + (ks > 1 ? 6 * bm : 0);
+    const uint64_t cost = rounds * steps * (std::min(bm, m) + bn) + 5 * bm * (ks - 1);
     if (cost < best_cost) {
       best_cost = cost;
       best = bm;
