@@ -19,7 +19,18 @@
 
 #include <stdint.h>
 
-#if defined(__GNUC__)
+/* Export control (reference include/ullm/hip.h:6-13).  A Windows DLL build
+ * defines ULLM_HIP_SHARED (and ULLM_HIP_BUILD while compiling the library);
+ * ELF builds compile with -fvisibility=hidden, so the public entry points
+ * carry default visibility explicitly, in the shared library and in the
+ * static archive alike. */
+#if defined(_WIN32) && defined(ULLM_HIP_SHARED)
+#if defined(ULLM_HIP_BUILD)
+#define ULLM_HIP_API __declspec(dllexport)
+#else
+#define ULLM_HIP_API __declspec(dllimport)
+#endif
+#elif defined(__GNUC__)
 #define ULLM_HIP_API __attribute__((visibility("default")))
 #else
 #define ULLM_HIP_API

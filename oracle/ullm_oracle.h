@@ -2,7 +2,7 @@
  * ullm_oracle.h -- CPU restatement of the quantized linear-layer path.
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP
- * kernels in ullm-project_amd/csrc are compared against.  Only tests/,
+ * kernels in ullm-project_amd/src are compared against.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
  * product library never links or calls it.
  *

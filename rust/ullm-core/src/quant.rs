@@ -3,7 +3,8 @@
 //! toolchain); the byte counts below are the ones tests/test_gpu_linear.py and
 //! bench.py use (FP8: N*K + 4N; AQ4: N*K/2 + 4*N*K/128).
 //!
-//! Wiring (reference crates/ullm-core/src/dtype.rs:55-122, op.rs:97-113):
+//! Wiring, as rust/patches/ullm-core.patch applies it (reference
+//! crates/ullm-core/src/dtype.rs:55-122, op.rs:97-113):
 //!
 //! 1. `mod quant; pub use quant::*;` in crates/ullm-core/src/lib.rs.
 //! 2. Two `Encoding` variants next to `Nvfp4`:

@@ -1,11 +1,13 @@
 // Bindings of the gfx950 library's linear-layer ABI (include/ullm/linear.h)
 // and weight-file ABI (include/ullm/weights_io.h), for
 // crates/ullm-hip-sys.  Not compiled in this build's container (no Rust
-// toolchain): the struct layouts are those the C layout probe of
-// tests/test_abi_host.py checks against the ctypes mirror, and belong in the
-// build.rs layout-parity probe (reference crates/ullm-hip-sys/build.rs:330-408).
+// toolchain).  tests/test_rust_bindings.py checks every constant, struct
+// layout and function signature here against the C headers, and
+// abi_layout_probe.rs prints the layouts for the patched build.rs's
+// comparison with the C++ probe (reference crates/ullm-hip-sys/build.rs:330-408).
 //
-// Wiring: `pub mod linear { include!("linear_bindings.rs"); }` in
+// Wiring (rust/patches/ullm-hip-sys.patch): `pub mod linear {
+// include!("linear_bindings.rs"); }` in
 // crates/ullm-hip-sys/src/lib.rs, next to the `evidence` module
 // (reference crates/ullm-hip-sys/src/lib.rs:8-13).  The evidence functions
 // keep their existing bindings (evidence_bindings.rs) unchanged; this
@@ -180,6 +182,23 @@ pub struct ullm_linear_weight_export_desc_t {
     pub stream: *mut c_void,
     pub reserved: [u64; 4],
 }
+
+pub const ULLM_ST_DTYPE_BOOL: u32 = 1;
+pub const ULLM_ST_DTYPE_U8: u32 = 2;
+pub const ULLM_ST_DTYPE_I8: u32 = 3;
+pub const ULLM_ST_DTYPE_F8_E4M3: u32 = 4;
+pub const ULLM_ST_DTYPE_F8_E5M2: u32 = 5;
+pub const ULLM_ST_DTYPE_U16: u32 = 6;
+pub const ULLM_ST_DTYPE_I16: u32 = 7;
+pub const ULLM_ST_DTYPE_F16: u32 = 8;
+pub const ULLM_ST_DTYPE_BF16: u32 = 9;
+pub const ULLM_ST_DTYPE_U32: u32 = 10;
+pub const ULLM_ST_DTYPE_I32: u32 = 11;
+pub const ULLM_ST_DTYPE_F32: u32 = 12;
+pub const ULLM_ST_DTYPE_U64: u32 = 13;
+pub const ULLM_ST_DTYPE_I64: u32 = 14;
+pub const ULLM_ST_DTYPE_F64: u32 = 15;
+pub const ULLM_ST_MAX_RANK: u32 = 8;
 
 #[repr(C)]
 pub struct ullm_safetensors_t {

@@ -2,7 +2,8 @@
 //! (reference crates/ullm-hip/src/lib.rs:496-505), for crates/ullm-hip.
 //! Not compiled in this build's container (no Rust toolchain).
 //!
-//! Wiring: `mod backend_support;` in crates/ullm-hip/src/lib.rs, and in
+//! Wiring (rust/patches/ullm-hip.patch): `mod backend_support;` in
+//! crates/ullm-hip/src/lib.rs, and in
 //! `impl Backend for HipBackend`:
 //!
 //! ```ignore

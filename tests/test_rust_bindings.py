@@ -1,0 +1,246 @@
+"""The checked-in Rust side of the boundary against the C headers (CPU only).
+
+No Rust toolchain exists in this container, so the checks restate what the
+patched crates/ullm-hip-sys/build.rs does with rustc (reference
+build.rs:330-408): the C++ layout probe's output is compared with layouts
+computed from the Rust declarations by the repr(C) rules, and every extern
+function, struct and constant of rust/ullm-hip-sys/src/linear_bindings.rs is
+compared with include/ullm/linear.h and weights_io.h.  The Rust patches
+against the reference crates are checked to apply to the reference tree.
+"""
+from __future__ import annotations
+
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import abi_parse as A
+
+ROOT = Path(__file__).resolve().parent.parent
+INC = ROOT / "include" / "ullm"
+SYS = ROOT / "rust" / "ullm-hip-sys" / "src"
+PROBE_SRC = ROOT / "ullm-project_amd" / "src" / "abi_layout_probe.cpp"
+GOLDEN = ROOT / "tests" / "golden"
+REFERENCE = Path("/root/reference")
+
+EXT_HEADERS = ("linear.h", "weights_io.h")
+
+
+def _c_text(*names):
+    return "".join((INC / n).read_text() for n in ("hip.h",) + tuple(names))
+
+
+@pytest.fixture(scope="module")
+def probe(tmp_path_factory):
+    exe = tmp_path_factory.mktemp("probe") / "abi_layout_probe"
+    # the flags the reference build.rs compiles its probe with (build.rs:334-345)
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-I", str(ROOT / "include"),
+                    str(PROBE_SRC), "-o", str(exe)], check=True)
+
+    def run(*args):
+        return subprocess.run([str(exe), *args], check=True, capture_output=True,
+                              text=True).stdout
+    return run
+
+
+def _rust_all():
+    text = (SYS / "linear_bindings.rs").read_text()
+    return A.rust_constants(text), A.rust_structs(text), A.rust_functions(text)
+
+
+def test_probe_matches_committed_layouts(probe):
+    """The header layouts are frozen: any change to a struct or constant of
+    linear.h / weights_io.h shows up here and must be made on purpose."""
+    assert probe("--extensions") == (GOLDEN / "abi_layout_extensions.txt").read_text()
+    assert probe() == (GOLDEN / "abi_layout_v1.txt").read_text()
+
+
+def test_probe_covers_every_struct_field_and_constant(probe):
+    """The probe lists every field of every struct and every constant of the
+    extension headers, in declaration order."""
+    text = _c_text(*EXT_HEADERS)
+    consts = A.c_constants(text)
+    structs = A.c_structs(text, consts)
+    ext_text = "".join((INC / n).read_text() for n in EXT_HEADERS)
+    ext_structs = A.c_structs(ext_text, consts)
+    ext_consts = A.c_constants(ext_text)
+    out = probe("--extensions").splitlines()
+    printed_consts = {l.split()[1].split("=")[0]: int(l.split("=")[1]) for l in out if l.startswith("const ")}
+    printed_layouts = {l.split()[1]: l for l in out if l.startswith("layout ")}
+    # header-guard-only names (ULLM_LINEAR_H ...) carry no value
+    assert printed_consts == ext_consts
+    assert set(printed_layouts) == set(ext_structs)
+    for name in ext_structs:
+        assert printed_layouts[name] == A.layout_line(name, structs), name
+
+
+def test_rust_layouts_equal_c_layouts(probe):
+    """repr(C) layouts of the Rust structs equal the C++ probe's figures, as
+    the patched build.rs requires of rustc's output."""
+    _, rstructs, _ = _rust_all()
+    printed = {l.split()[1]: l for l in probe("--extensions").splitlines() if l.startswith("layout ")}
+    assert set(rstructs) - {"ullm_linear_weight_t", "ullm_safetensors_t"} == set(printed)
+    for name, line in printed.items():
+        assert A.layout_line(name, rstructs) == line, name
+
+
+def test_rust_struct_fields_equal_c_fields():
+    """Field names, order and types, not only offsets."""
+    text = _c_text(*EXT_HEADERS)
+    cstructs = A.c_structs(text, A.c_constants(text))
+    _, rstructs, _ = _rust_all()
+    for name, fields in rstructs.items():
+        if name in ("ullm_linear_weight_t", "ullm_safetensors_t"):
+            assert fields == [("_private", ("array", "u8", 0))], name
+            assert re.search(rf"typedef struct {name} {name};", text), name
+            continue
+        assert fields == cstructs[name], name
+
+
+def test_rust_constants_equal_c_constants():
+    ext_text = "".join((INC / n).read_text() for n in EXT_HEADERS)
+    cconsts = A.c_constants(ext_text)
+    rconsts, _, _ = _rust_all()
+    # statuses 8..12 are bound once, in the reference's evidence_bindings.rs
+    evidence = {k: v for k, v in cconsts.items() if k.startswith("ULLM_STATUS_HIP_")}
+    assert evidence == {"ULLM_STATUS_HIP_TIMEOUT": 8, "ULLM_STATUS_HIP_INVALID_HANDLE": 9,
+                        "ULLM_STATUS_HIP_ZERO_DISPATCH": 10, "ULLM_STATUS_HIP_RUNTIME_ERROR": 11,
+                        "ULLM_STATUS_HIP_DISPATCH_CONTRACT": 12}
+    expected = {k: v for k, v in cconsts.items() if k not in evidence}
+    assert rconsts == expected
+
+
+def test_rust_functions_equal_c_prototypes():
+    cfuncs = A.c_functions("".join((INC / n).read_text() for n in EXT_HEADERS))
+    _, _, rfuncs = _rust_all()
+    assert set(rfuncs) == set(cfuncs)
+    for name, (ret, args) in cfuncs.items():
+        rret, rargs = rfuncs[name]
+        assert rret == ret == "ullm_status_t", name
+        assert rargs == args, name
+
+
+def test_rust_probe_prints_what_the_cxx_probe_prints(probe):
+    """rust/ullm-hip-sys/src/abi_layout_probe.rs names the same constants,
+    structs and fields in the same order as the C++ probe, in both modes, so
+    that build.rs's comparison of the two outputs is line for line."""
+    src = (SYS / "abi_layout_probe.rs").read_text()
+
+    def rust_items(fn):
+        body = src.split(f"fn {fn}() {{")[1].split("\n}\n")[0]
+        items = []
+        for m in re.finditer(r"consts!\((.*?)\);|layout!\((\w+) \{(.*?)\}\);", body, flags=re.S):
+            if m.group(1) is not None:
+                items += [f"const {c.strip()}" for c in m.group(1).split(",") if c.strip()]
+            else:
+                fields = [f.strip() for f in m.group(3).split(",") if f.strip()]
+                items.append(f"layout {m.group(2)} " + " ".join(fields))
+        return items
+
+    def cxx_items(out):
+        items = []
+        for line in out.splitlines():
+            parts = line.split()
+            if parts[0] == "const":
+                items.append("const " + parts[1].split("=")[0])
+            else:
+                fields = [p.split("=")[0] for p in parts[2:] if not p.startswith(("size=", "align="))]
+                items.append(f"layout {parts[1]} " + " ".join(fields))
+        return items
+
+    assert rust_items("print_v1") == cxx_items(probe())
+    assert rust_items("print_extensions") == cxx_items(probe("--extensions"))
+
+
+def test_integration_doc_lists_every_binding():
+    """INTEGRATION.md points at the binding file instead of restating it, and
+    names every exported function of the extension."""
+    doc = (ROOT / "INTEGRATION.md").read_text()
+    assert "rust/ullm-hip-sys/src/linear_bindings.rs" in doc
+    _, _, rfuncs = _rust_all()
+    missing = [f for f in rfuncs if f not in doc]
+    assert not missing, missing
+
+
+# ------------------------------------------------------- reference patches
+PATCHES = ROOT / "rust" / "patches"
+NEW_FILES = {
+    "crates/ullm-core/src/quant.rs": ROOT / "rust/ullm-core/src/quant.rs",
+    "crates/ullm-hip/src/backend_support.rs": ROOT / "rust/ullm-hip/src/backend_support.rs",
+    "crates/ullm-hip/src/linear.rs": ROOT / "rust/ullm-hip/src/linear.rs",
+    "crates/ullm-hip-sys/src/linear_bindings.rs": SYS / "linear_bindings.rs",
+    "crates/ullm-hip-sys/src/abi_layout_probe.rs": SYS / "abi_layout_probe.rs",
+}
+
+
+@pytest.fixture(scope="module")
+def patched_tree(tmp_path_factory):
+    if not (REFERENCE / "crates").is_dir():
+        pytest.skip("reference tree not present (CPU container only)")
+    tree = tmp_path_factory.mktemp("ref")
+    shutil.copytree(REFERENCE / "crates", tree / "crates")
+    for patch in sorted(PATCHES.glob("*.patch")):
+        subprocess.run(["git", "apply", "--check", str(patch)], cwd=tree, check=True)
+        subprocess.run(["git", "apply", str(patch)], cwd=tree, check=True)
+    for rel, src in NEW_FILES.items():
+        shutil.copyfile(src, tree / rel)
+    return tree
+
+
+def test_patches_apply_and_wire_the_new_modules(patched_tree):
+    t = patched_tree
+    dtype = (t / "crates/ullm-core/src/dtype.rs").read_text()
+    assert "Fp8RowScaled { row_len: usize, scale_dtype: DType }" in dtype
+    assert "crate::quant::aq4_bytes(elements)" in dtype
+    assert "mod quant;" in (t / "crates/ullm-core/src/lib.rs").read_text()
+    op = (t / "crates/ullm-core/src/op.rs").read_text()
+    assert "crate::quant::is_quantized_matmul(" in op
+    hip = (t / "crates/ullm-hip/src/lib.rs").read_text()
+    assert "mod backend_support;" in hip and "pub mod linear;" in hip
+    assert "numerical_execution: true" in hip
+    assert "backend_support::quantized_matmul_support(operation)" in hip
+    sys_lib = (t / "crates/ullm-hip-sys/src/lib.rs").read_text()
+    assert 'include!("linear_bindings.rs")' in sys_lib
+    build = (t / "crates/ullm-hip-sys/build.rs").read_text()
+    assert 'target == "gfx950"' in build and "co_v6,wave64" in build
+    assert "verify_extension_bindings(&rust_layout_probe, &out_dir);" in build
+    # amdhip64 is linked unconditionally now
+    assert re.search(r'\n    println!\("cargo:rustc-link-lib=dylib=amdhip64"\);', build)
+
+
+def test_patched_v1_bindings_match_the_probe(patched_tree, probe):
+    """The reference's v1 bindings (minor version bumped by the patch) against
+    this library's hip.h, as build.rs's own probe comparison does."""
+    text = (patched_tree / "crates/ullm-hip-sys/src/bindings.rs").read_text()
+    rconsts = A.rust_constants(text)
+    rstructs = A.rust_structs(text)
+    for line in probe().splitlines():
+        parts = line.split()
+        if parts[0] == "const":
+            name, value = parts[1].split("=")
+            assert rconsts[name] == int(value), name
+        else:
+            assert A.layout_line(parts[1], rstructs) == line, parts[1]
+    # every v1 function keeps its reference signature
+    cfuncs = A.c_functions((INC / "hip.h").read_text())
+    rfuncs = A.rust_functions(text)
+    for name, (ret, args) in cfuncs.items():
+        assert rfuncs[name] == (ret, args), name
+
+
+def test_rust_probe_resolves_its_modules(patched_tree):
+    """abi_layout_probe.rs finds bindings.rs, evidence_bindings.rs and
+    linear_bindings.rs next to it, and every constant it prints is declared
+    in one of them."""
+    d = patched_tree / "crates/ullm-hip-sys/src"
+    src = (d / "abi_layout_probe.rs").read_text()
+    for f in re.findall(r'#\[path = "([^"]+)"\]', src) + re.findall(r'include!\("([^"]+)"\)', src):
+        assert (d / f).is_file(), f
+    declared = {}
+    for f in ("bindings.rs", "evidence_bindings.rs", "linear_bindings.rs"):
+        declared.update(A.rust_constants((d / f).read_text()))
+    for c in re.findall(r"^\s+(ULLM_\w+),$", src, flags=re.M):
+        assert c in declared, c

@@ -15,7 +15,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-CSRC = PKG / "csrc"
+CSRC = PKG / "src"
 BUILD = PKG / "_build"
 LIB = PKG / "lib" / "libullm_hip.so"
 # Measurement aid of bench.py (a streaming-read floor kernel); not linked
