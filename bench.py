@@ -149,17 +149,25 @@ def bench_gemm(r, m, n, k, steps, warmup):
     ms_step, us_call, mode = r.time_sweep(calls, steps, warmup)
     tflops = 2.0 * m * n * k / (us_call * 1e-6) / 1e12
     # End to end from bf16 activations: per-token quantization into the
-    # caller's workspace, then the GEMM (two kernels per call).
+    # caller's workspace, then the GEMM (two kernels per call).  The bf16
+    # activations rotate over enough copies (> 256 MB) that each call's
+    # quantization reads them from HBM, as a prefill step would.
+    xcopies = max(16, -(-(256 << 20) // (2 * m * k)) + 1)
+    xs_b = [torch.randn((m, k), generator=g, device=r.dev).to(torch.bfloat16)
+            for _ in range(xcopies)]
     wsb = torch.empty((ws[0].workspace_size(m, mode=uh.ACT_FP8_PER_TOKEN),),
                       dtype=torch.uint8, device=r.dev)
-    calls = [(lambda w=w: w.forward(x, y, mode=uh.ACT_FP8_PER_TOKEN,
-                                    workspace=wsb)) for w in ws]
+    ncalls = max(copies, xcopies)
+    calls = [(lambda w=ws[i % copies], xb=xs_b[i % xcopies]:
+              w.forward(xb, y, mode=uh.ACT_FP8_PER_TOKEN, workspace=wsb))
+             for i in range(ncalls)]
     _, us_e2e, _ = r.time_sweep(calls, steps, warmup)
+    del xs_b
     for w in ws:
         w.destroy()
     return {"m": m, "n": n, "k": k, "copies": copies, "us_per_launch": us_call,
             "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
-            "us_with_act_quant": us_e2e,
+            "us_with_act_quant": us_e2e, "act_copies": xcopies,
             "TFLOPS_with_act_quant": 2.0 * m * n * k / (us_e2e * 1e-6) / 1e12,
             "timing": mode}
 
@@ -295,28 +303,52 @@ def measured_traffic(workload):
     return None
 
 
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# Threads the CPU leg uses: the host share of one GPU on the GPU boxes this
+# runs on (16 threads per GPU), or fewer when the process may use fewer CPUs.
+CPU_SHARE_THREADS = 16
+
+
 def cpu_baseline(seconds=10.0):
-    """The oracle's AQ4 matvec on the host cores, same shape, bounded time."""
+    """The oracle's AQ4 matvec on the host cores, same shape, bounded time.
+    The oracle source is compiled here with -march=native (for this host's
+    CPU), OpenMP over output rows."""
+    import tempfile
     import numpy as np
     from oracle import oracle as orc
     m, n, k = 1, 14336, 4096
-    threads = min(16, os.cpu_count() or 1)
-    rs = np.random.default_rng(0)
-    w = (rs.standard_normal((n, k)) * 0.02).astype(np.float32)
-    p, s, z = orc.aq4_quantize(w)
-    xb = orc.bf16_from_f32(rs.standard_normal((m, k)).astype(np.float32))
-    orc.aq4_gemv(xb, p, s, z, threads=threads)
-    t0 = time.perf_counter()
-    calls = 0
-    while time.perf_counter() - t0 < seconds:
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(CPU_SHARE_THREADS, affinity)
+    with tempfile.TemporaryDirectory() as tmp:
+        orc.use_library(orc.build_native(Path(tmp)))
+        rs = np.random.default_rng(0)
+        w = (rs.standard_normal((n, k)) * 0.02).astype(np.float32)
+        p, s, z = orc.aq4_quantize(w)
+        xb = orc.bf16_from_f32(rs.standard_normal((m, k)).astype(np.float32))
         orc.aq4_gemv(xb, p, s, z, threads=threads)
-        calls += 1
-    dt = (time.perf_counter() - t0) / calls
+        t0 = time.perf_counter()
+        calls = 0
+        while time.perf_counter() - t0 < seconds:
+            orc.aq4_gemv(xb, p, s, z, threads=threads)
+            calls += 1
+        dt = (time.perf_counter() - t0) / calls
     return {"value": aq4_bytes(m, n, k) / dt / 1e9, "unit": "GB/s",
             "cores": threads, "kind": "port",
+            "host_logical_cpus": os.cpu_count(), "affinity_cpus": affinity,
+            "cpu_model": _cpu_model(), "build": "gcc -O3 -march=native -fopenmp",
             "sample": f"{calls} AQ4 matvecs M=1 K=4096 N=14336 "
-                      f"(oracle fp32 loop, OpenMP {threads} threads, "
-                      f"{dt * 1e3:.1f} ms each)"}
+                      f"(oracle fp32 loop, OpenMP {threads} threads: the 16-thread host "
+                      f"share of one GPU, capped by the {affinity} CPUs this process "
+                      f"may use; {dt * 1e3:.1f} ms each)"}
 
 
 def main():

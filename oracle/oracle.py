@@ -34,6 +34,23 @@ def build(force: bool = False) -> Path:
     return LIB_PATH
 
 
+def build_native(out_dir: Path) -> Path:
+    """Compile the same source with ``-march=native`` for the machine this runs
+    on (the CPU-baseline timing copy; built where it is timed, since the
+    container that builds the tree and the GPU box have different CPUs)."""
+    out = Path(out_dir) / "liboracle_native.so"
+    flags = [f for f in CFLAGS if not f.startswith("-march=")] + ["-march=native"]
+    subprocess.run(["gcc", *flags, *map(str, SOURCES), "-o", str(out), "-lm"], check=True)
+    return out
+
+
+def use_library(path: Path) -> None:
+    """Route every oracle call through the library at ``path`` (a build of the
+    same source, e.g. build_native's)."""
+    global _lib
+    _lib = _load(Path(path))
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
 _F = ctypes.c_float
@@ -45,35 +62,39 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = ctypes.CDLL(str(LIB_PATH))
-        sig = {
-            "orc_e4m3_from_f32": (ctypes.c_uint8, [_F]),
-            "orc_e4m3_to_f32": (_F, [ctypes.c_uint8]),
-            "orc_bf16_from_f32": (ctypes.c_uint16, [_F]),
-            "orc_bf16_to_f32": (_F, [ctypes.c_uint16]),
-            "orc_f16_from_f32": (ctypes.c_uint16, [_F]),
-            "orc_f16_to_f32": (_F, [ctypes.c_uint16]),
-            "orc_e4m3_from_f32_n": (None, [_P, _P, _I]),
-            "orc_bf16_from_f32_n": (None, [_P, _P, _I]),
-            "orc_f16_from_f32_n": (None, [_P, _P, _I]),
-            "orc_fp8_quantize_rows": (None, [_P, _I, _I, _P, _P]),
-            "orc_fp8_dequantize": (None, [_P, _P, _I, _I, _P]),
-            "orc_aq4_quantize": (None, [_P, _I, _I, _P, _P, _P]),
-            "orc_aq4_dequantize": (None, [_P, _P, _P, _I, _I, _P]),
-            "orc_fp8_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _F, _P, _P, ctypes.c_int]),
-            "orc_aq4_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
-            "orc_act_quantize": (None, [_I, _I, _P, _I, _P, _P]),
-            "orc_bf16_add": (None, [_I, _P, _P, _P]),
-            "orc_fp8_gemm": (None, [_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
-            "orc_silu_mul": (None, [_I, _I, _P, _P]),
-            "orc_max_threads": (ctypes.c_int, []),
-        }
-        for name, (res, args) in sig.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = L
+        _lib = _load(LIB_PATH)
     return _lib
+
+
+def _load(path: Path) -> ctypes.CDLL:
+    L = ctypes.CDLL(str(path))
+    sig = {
+        "orc_e4m3_from_f32": (ctypes.c_uint8, [_F]),
+        "orc_e4m3_to_f32": (_F, [ctypes.c_uint8]),
+        "orc_bf16_from_f32": (ctypes.c_uint16, [_F]),
+        "orc_bf16_to_f32": (_F, [ctypes.c_uint16]),
+        "orc_f16_from_f32": (ctypes.c_uint16, [_F]),
+        "orc_f16_to_f32": (_F, [ctypes.c_uint16]),
+        "orc_e4m3_from_f32_n": (None, [_P, _P, _I]),
+        "orc_bf16_from_f32_n": (None, [_P, _P, _I]),
+        "orc_f16_from_f32_n": (None, [_P, _P, _I]),
+        "orc_fp8_quantize_rows": (None, [_P, _I, _I, _P, _P]),
+        "orc_fp8_dequantize": (None, [_P, _P, _I, _I, _P]),
+        "orc_aq4_quantize": (None, [_P, _I, _I, _P, _P, _P]),
+        "orc_aq4_dequantize": (None, [_P, _P, _P, _I, _I, _P]),
+        "orc_fp8_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _F, _P, _P, ctypes.c_int]),
+        "orc_aq4_gemv": (None, [_I, _I, _I, _P, _I, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
+        "orc_act_quantize": (None, [_I, _I, _P, _I, _P, _P]),
+        "orc_bf16_add": (None, [_I, _P, _P, _P]),
+        "orc_fp8_gemm": (None, [_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, ctypes.c_int]),
+        "orc_silu_mul": (None, [_I, _I, _P, _P]),
+        "orc_max_threads": (ctypes.c_int, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
 
 
 def _p(a: np.ndarray | None):
