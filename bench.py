@@ -162,12 +162,19 @@ def bench_gemm(r, m, n, k, steps, warmup):
               w.forward(xb, y, mode=uh.ACT_FP8_PER_TOKEN, workspace=wsb))
              for i in range(ncalls)]
     _, us_e2e, _ = r.time_sweep(calls, steps, warmup)
+    # The quantization alone over the same rotated activations (HBM-fed).
+    xq_b = torch.empty((m, k), dtype=torch.uint8, device=r.dev)
+    xs_s = torch.empty((m,), dtype=torch.float32, device=r.dev)
+    calls = [(lambda xb=xb: uh.quantize_activations(xb, xq_b, xs_s, stream=r.stream))
+             for xb in xs_b]
+    _, us_quant, _ = r.time_sweep(calls, steps, warmup)
     del xs_b
     for w in ws:
         w.destroy()
     return {"m": m, "n": n, "k": k, "copies": copies, "us_per_launch": us_call,
             "TFLOPS": tflops, "frac_fp8_peak": tflops / FP8_PEAK_TFLOPS,
             "us_with_act_quant": us_e2e, "act_copies": xcopies,
+            "us_act_quant_alone": us_quant,
             "TFLOPS_with_act_quant": 2.0 * m * n * k / (us_e2e * 1e-6) / 1e12,
             "timing": mode}
 

@@ -829,12 +829,19 @@ def add_quantize_activations(a, b, out=None, stream=None):
     return xq, xs
 
 
-def quantize_activations(x, stream=None):
-    """Per-token E4M3 quantization: returns (xq uint8 [M][K], scales f32 [M])."""
+def quantize_activations(x, xq=None, xs=None, stream=None):
+    """Per-token E4M3 quantization: returns (xq uint8 [M][K], scales f32 [M]),
+    into the given contiguous outputs when passed."""
     import torch
     m, k = x.shape
-    xq = torch.empty((m, k), dtype=torch.uint8, device=x.device)
-    xs = torch.empty((m,), dtype=torch.float32, device=x.device)
+    if xq is None:
+        xq = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+    if xs is None:
+        xs = torch.empty((m,), dtype=torch.float32, device=x.device)
+    if xq.shape != (m, k) or not xq.is_contiguous() or xq.dtype != torch.uint8:
+        raise ValueError("xq must be a contiguous uint8 [M][K] tensor")
+    if xs.shape != (m,) or xs.dtype != torch.float32:
+        raise ValueError("xs must be a float32 [M] tensor")
     d = new(ActQuantDesc, m=m, k=k, x=_ptr(x), x_row_stride=x.stride(0),
             xq=_ptr(xq), x_scales=_ptr(xs), stream=_stream(stream))
     s = _Sink()
