@@ -53,6 +53,40 @@ def _compile(src: str) -> Path:
     return out
 
 
+CMAKE_BUILD = BUILD / "cmake"
+ARCHIVE = CMAKE_BUILD / "libullm_hip_stub.a"
+# A C program linked against the static archive (tests/archive_check.c), run
+# by tests/test_gpu_archive.py on the GPU box.
+ARCHIVE_CHECK = PKG / "lib" / "ullm_archive_check"
+
+
+def build_static() -> Path:
+    """Build the CMake project's static target ullm_hip_stub with the
+    arguments the reference's ullm-hip-sys build.rs passes, and link
+    tests/archive_check.c against it as a Rust binary would link the crate
+    (the archive, amdhip64, stdc++)."""
+    rocm = Path("/opt/rocm")
+    subprocess.run(
+        ["cmake", "-S", str(PKG), "-B", str(CMAKE_BUILD), "-G", "Unix Makefiles",
+         "-DCMAKE_BUILD_TYPE=release", f"-DCMAKE_ARCHIVE_OUTPUT_DIRECTORY={CMAKE_BUILD}",
+         f"-DROCM_PATH={rocm}", f"-DCMAKE_HIP_COMPILER={rocm}/bin/amdclang++",
+         "-DCMAKE_HIP_ARCHITECTURES=gfx950", "-DULLM_HIP_COMPILE_TARGET=gfx950",
+         "-DULLM_ENABLE_HIP_COMPILE_PROBE=OFF", "-DULLM_ENABLE_HIP_RUNTIME=ON"],
+        check=True, capture_output=True, text=True)
+    r = subprocess.run(["cmake", "--build", str(CMAKE_BUILD), "--target", "ullm_hip_stub",
+                        "-j8"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"cmake build of ullm_hip_stub failed:\n{r.stdout[-4000:]}{r.stderr[-4000:]}")
+    tmp = ARCHIVE_CHECK.with_suffix(".tmp")
+    subprocess.run(
+        ["gcc", "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+         f"-I{ROOT / 'include'}", f"-I{rocm / 'include'}", str(ROOT / "tests" / "archive_check.c"),
+         f"-L{CMAKE_BUILD}", "-lullm_hip_stub", f"-L{rocm / 'lib'}", "-lamdhip64", "-lstdc++",
+         "-lm", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(tmp)], check=True)
+    os.replace(tmp, ARCHIVE_CHECK)
+    return ARCHIVE
+
+
 def build() -> Path:
     """Compile every source (always) and link libullm_hip.so."""
     BUILD.mkdir(exist_ok=True)
