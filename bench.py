@@ -14,7 +14,8 @@ Extra configurations (FP8 matvec, the FP8 small-M sweep M = 1..32 over the
 four Llama-3-8B layer shapes, a plain streaming-read floor at the headline
 sizes, the M=2048 FP8 GEMM and the 32-layer AQ4 decode stack; "gemm_shapes"
 adds the other prefill projections, short prompts (M = 256, 512) and M < 128, "vendor_gemm" the same FP8
-GEMMs through hipBLASLt for reference) are reported under "configs".  The CPU
+GEMMs through hipBLASLt for reference, "floor_sweep" every read shape of the
+read-floor kernel at the headline's bytes) are reported under "configs".  The CPU
 baseline is this build's own C restatement (oracle/), not a reference CPU
 path: the reference has none.
 
@@ -252,7 +253,7 @@ def bench_read_floor(r, nbytes, steps, warmup):
     g.manual_seed(99)
     bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), generator=g,
                           device=r.dev, dtype=torch.int32) for _ in range(copies)]
-    sink = torch.empty(((nbytes >> 12) + 1,), dtype=torch.int32, device=r.dev)
+    sink = torch.empty(((nbytes >> 10) + 1,), dtype=torch.int32, device=r.dev)
 
     def call(b, shape):
         st = fn(b.data_ptr(), nbytes, shape, sink.data_ptr(),
@@ -275,6 +276,49 @@ def bench_read_floor(r, nbytes, steps, warmup):
             "us_per_launch": us_call, "GB_s": gbs,
             "frac_hbm": gbs / HBM_PEAK_GBS, "timing": mode,
             "kernel": f"stream_read_kernel ({name})"}
+
+
+def bench_read_sweep(r, nbytes, steps, warmup):
+    """Every read shape of libullm_bench.so's sweep (1-16 waves per workgroup,
+    1-32 1 KiB loads in flight per wave, 1-32 KiB per wave) over rotated
+    random buffers of `nbytes`: how far the floor the `floor` leg reports is
+    from the fastest plain read of those bytes this harness can time."""
+    import ctypes
+    torch = r.torch
+    bench_lib = ctypes.CDLL(str(ROOT / "ullm-project_amd" / "lib" / "libullm_bench.so"))
+    fn = bench_lib.ullm_bench_stream_read_shape
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                   ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    fn.restype = ctypes.c_int
+    nbytes = nbytes // 16 * 16
+    copies = max(4, -(-ROTATE_BYTES // nbytes))
+    g = torch.Generator(device=r.dev)
+    g.manual_seed(98)
+    bufs = [torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), generator=g,
+                          device=r.dev, dtype=torch.int32) for _ in range(copies)]
+    sink = torch.empty(((nbytes >> 10) + 1,), dtype=torch.int32, device=r.dev)
+
+    def call(b, w, d, c):
+        st = fn(b.data_ptr(), nbytes, w, d, c, sink.data_ptr(),
+                torch.cuda.current_stream().cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"stream_read_shape launch failed: {st}")
+
+    shapes = []
+    for w in (1, 2, 4, 8, 16):
+        for d in (1, 2, 4, 8, 16, 32):
+            for kib in (1, 2, 4, 8, 16, 32):
+                if kib % d == 0:
+                    calls = [(lambda b=b, w=w, d=d, c=kib * 1024: call(b, w, d, c)) for b in bufs]
+                    _, us, _ = r.time_sweep(calls, steps, warmup)
+                    shapes.append((us, w, d, kib))
+    del bufs
+    shapes.sort()
+    return {"bytes_per_launch": nbytes, "copies": copies, "shapes": len(shapes),
+            "best_us": shapes[0][0], "best_GB_s": nbytes / (shapes[0][0] * 1e-6) / 1e9,
+            "worst_us": shapes[-1][0],
+            "fastest": [{"us": round(u, 3), "waves": w, "depth": d, "kib_per_wave": k}
+                        for u, w, d, k in shapes[:8]]}
 
 
 def bench_stack(r, steps, warmup):
@@ -420,6 +464,10 @@ def main():
             configs[f"read_floor_{name}"] = bench_read_floor(
                 r, nbytes, args.steps, args.warmup)
             log("read floor", name, configs[f"read_floor_{name}"])
+    if "floor_sweep" in want:
+        configs["read_sweep_aq4_m1_k4096_n14336"] = bench_read_sweep(
+            r, aq4_bytes(1, 14336, 4096), max(10, args.steps // 2), 2)
+        log("read sweep:", configs["read_sweep_aq4_m1_k4096_n14336"])
     if "stack_proj" in want:
         # The stack's projections one at a time (AQ4, M = 8, contiguous x),
         # over rotated copies like the headline.

@@ -56,7 +56,7 @@ int launch(const void *src, uint64_t bytes, uint32_t chunk, uint32_t *sink,
 
 // Shape `shape` (0: 4 waves x 4 loads over 4 KiB per wave; 1: 4 x 8 over
 // 8 KiB; 2: 8 x 8 over 8 KiB) reads `bytes` (a multiple of 16) at `src`;
-// `sink` must hold one u32 per 4 KiB of input.  Returns the launch status.
+// `sink` must hold one u32 per 1 KiB of input.  Returns the launch status.
 extern "C" __attribute__((visibility("default"))) int ullm_bench_stream_read(
     const void *src, uint64_t bytes, uint32_t shape, uint32_t *sink, void *stream) {
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -64,5 +64,40 @@ extern "C" __attribute__((visibility("default"))) int ullm_bench_stream_read(
     case 0: return launch<4, 4>(src, bytes, 4096, sink, s);
     case 1: return launch<4, 8>(src, bytes, 8192, sink, s);
     default: return launch<8, 8>(src, bytes, 8192, sink, s);
+  }
+}
+
+// The sweep of read shapes behind the floor: `waves` per workgroup (1, 2, 4,
+// 8 or 16), `depth` independent 1 KiB loads in flight per wave (1, 2, 4, 8,
+// 16 or 32), `chunk` bytes per wave (a multiple of depth x 1 KiB),
+// non-temporal loads.  Returns hipErrorInvalidValue for any other shape.
+template <int W>
+int launch_depth(const void *src, uint64_t bytes, uint32_t depth, uint32_t chunk,
+                 uint32_t *sink, hipStream_t s) {
+  switch (depth) {
+    case 1: return launch<W, 1>(src, bytes, chunk, sink, s);
+    case 2: return launch<W, 2>(src, bytes, chunk, sink, s);
+    case 4: return launch<W, 4>(src, bytes, chunk, sink, s);
+    case 8: return launch<W, 8>(src, bytes, chunk, sink, s);
+    case 16: return launch<W, 16>(src, bytes, chunk, sink, s);
+    case 32: return launch<W, 32>(src, bytes, chunk, sink, s);
+    default: return int(hipErrorInvalidValue);
+  }
+}
+
+extern "C" __attribute__((visibility("default"))) int ullm_bench_stream_read_shape(
+    const void *src, uint64_t bytes, uint32_t waves, uint32_t depth, uint32_t chunk,
+    uint32_t *sink, void *stream) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (chunk == 0 || chunk % (depth * 1024u) != 0) {
+    return int(hipErrorInvalidValue);
+  }
+  switch (waves) {
+    case 1: return launch_depth<1>(src, bytes, depth, chunk, sink, s);
+    case 2: return launch_depth<2>(src, bytes, depth, chunk, sink, s);
+    case 4: return launch_depth<4>(src, bytes, depth, chunk, sink, s);
+    case 8: return launch_depth<8>(src, bytes, depth, chunk, sink, s);
+    case 16: return launch_depth<16>(src, bytes, depth, chunk, sink, s);
+    default: return int(hipErrorInvalidValue);
   }
 }
