@@ -336,6 +336,24 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
   if (threadIdx.x == 0) {
     xs[row] = a;
   }
+  // x / a through the row's reciprocal: q0 = x * r, then one residual step
+  // q = q0 + (x - q0 a) r with fused multiply-adds (r = 1 / a correctly
+  // rounded, once per row).  For a >= 2^-100 this gives the same E4M3 code
+  // as the correctly rounded quotient for every bf16 x with |x| <= max|x|:
+  // checked exhaustively over every finite bf16 row maximum and every such
+  // x (tests/test_act_quant_division.py).  The quotients that differ in the
+  // last fp32 bit lie far below the smallest E4M3 code, and an exact zero
+  // keeps its sign (q0).  Rows with a smaller scale divide.
+  const float rcp = 1.0f / a;
+  const bool via_rcp = a >= 0x1p-100f;
+  auto quot = [&](float x) {
+    if (!via_rcp) {
+      return x / a;
+    }
+    const float q0 = x * rcp;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, a, x), rcp, q0);
+    return q0 == 0.0f ? q0 : q1;
+  };
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
@@ -352,7 +370,7 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t ww = w[2 * d + e / 2];
-            f[e] = bf16_to_f32(uint16_t(e % 2 ? ww >> 16 : ww & 0xffffu)) / a;
+            f[e] = quot(bf16_to_f32(uint16_t(e % 2 ? ww >> 16 : ww & 0xffffu)));
           }
           s16x2 r = {0, 0};
           r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, f[0], f[1], 1.0f, false);
