@@ -27,7 +27,9 @@ def _check(orc, a_bits, b_bits, xq, xs, s=None):
         assert np.all((got[nan] & 0x7FFF) > 0x7F80)
 
 
-@pytest.mark.parametrize("m,k", [(2048, 4096), (7, 14336), (5, 1001), (3, 24)])
+# 512-thread vector path: one, four and eight chunks per thread; K = 1001
+# takes the scalar kernel
+@pytest.mark.parametrize("m,k", [(2048, 4096), (7, 14336), (2, 32768), (5, 1001), (3, 24)])
 def test_add_quantize_parity(uh, orc, gpu, m, k):
     a_bits = activations_bf16(orc, m, k, tag=m + 700)
     b_bits = activations_bf16(orc, m, k, tag=m + 701)

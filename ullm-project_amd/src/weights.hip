@@ -16,6 +16,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
+template <int BLOCK = kBlock>
 __device__ float block_max(float v, float *red) {
   v = wave_max(v);
   const int wave = threadIdx.x / kWave;
@@ -24,7 +25,7 @@ __device__ float block_max(float v, float *red) {
   }
   __syncthreads();
   float r = red[0];
-  for (int i = 1; i < kBlock / kWave; ++i) {
+  for (int i = 1; i < BLOCK / kWave; ++i) {
     r = fmaxf(r, red[i]);
   }
   return r;
@@ -275,11 +276,17 @@ __global__ __launch_bounds__(kBlock) void act_quant_kernel(
 // multiple of 8: each thread keeps CH chunks of 8 bf16 of its row in
 // registers (one 16-byte load each), so the row is read once, and writes 8
 // codes per store.  The per-element arithmetic is that of act_quant_kernel.
+// Workgroups of 256 threads, or 512 with the residual add (two input
+// streams): measured on MI355X at M = 2048, K = 4096, the plain quantize
+// takes 7.4 us with 256 threads against 8.3 with 512 and 8.1 with 128; the
+// fused add 14.0 us with 512 against 14.8 with 256.
+constexpr int kAddBlock = 512;
 template <int CH, bool ADD>
-__global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
+__global__ __launch_bounds__(ADD ? kAddBlock : kBlock) void act_quant_vec_kernel(
     const uint16_t *x, uint64_t ldx, uint64_t k, uint8_t *__restrict__ xq,
     float *__restrict__ xs, AddIn add) {
-  __shared__ float red[kBlock / kWave];
+  constexpr int kT = ADD ? kAddBlock : kBlock;
+  __shared__ float red[kT / kWave];
   const uint64_t row = blockIdx.x;
   const uint16_t *src = x + row * ldx;
   u32x4 v[CH];
@@ -288,7 +295,7 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
   u16x2 mx = {0, 0};
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
+    const uint64_t idx = (uint64_t(c) * kT + threadIdx.x) * 8;
     v[c] = idx < k ? *reinterpret_cast<const u32x4 *>(src + idx)
                    : u32x4{0u, 0u, 0u, 0u};
     if constexpr (ADD) {
@@ -315,7 +322,7 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
     }
   }
   const uint32_t mb = mx.x > mx.y ? mx.x : mx.y;
-  float amax = block_max(mb >= 0x7f80u ? __builtin_inff() : bits_f32(mb << 16), red);
+  float amax = block_max<kT>(mb >= 0x7f80u ? __builtin_inff() : bits_f32(mb << 16), red);
   const bool finite = amax != __builtin_inff();
   if (!finite) {
     // A row holding inf or NaN: max|x| over the non-NaN values, as fmaxf.
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
         am = fmaxf(am, fabsf(bf16_to_f32(uint16_t(w[e] >> 16))));
       }
     }
-    amax = block_max(am, red);
+    amax = block_max<kT>(am, red);
   }
   const float a = amax / 448.0f;
   if (threadIdx.x == 0) {
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(kBlock) void act_quant_vec_kernel(
   };
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const uint64_t idx = (uint64_t(c) * kBlock + threadIdx.x) * 8;
+    const uint64_t idx = (uint64_t(c) * kT + threadIdx.x) * 8;
     if (idx < k) {
       const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
       uint32_t out[2] = {0u, 0u};
@@ -470,13 +477,14 @@ hipError_t launch_act_quant_t(const uint16_t *x, uint64_t ldx, uint64_t m,
     vec = vec && a16(add.b) && add.ldb % 8 == 0 &&
           (add.sum == nullptr || (a16(add.sum) && add.lds % 8 == 0));
   }
-  const uint64_t chunks = (k / 8 + kBlock - 1) / kBlock;  // per thread
+  const int threads = ADD ? kAddBlock : kBlock;
+  const uint64_t chunks = (k / 8 + threads - 1) / threads;  // per thread
   if (vec && chunks <= 8) {
     auto kernel = chunks <= 1   ? act_quant_vec_kernel<1, ADD>
                   : chunks <= 2 ? act_quant_vec_kernel<2, ADD>
                   : chunks <= 4 ? act_quant_vec_kernel<4, ADD>
                                 : act_quant_vec_kernel<8, ADD>;
-    hipLaunchKernelGGL(kernel, dim3(m), dim3(kBlock), 0, s, x, ldx, k, xq, xs, add);
+    hipLaunchKernelGGL(kernel, dim3(m), dim3(threads), 0, s, x, ldx, k, xq, xs, add);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(act_quant_kernel<ADD>, dim3(m), dim3(kBlock), 0, s, x, ldx,
