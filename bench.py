@@ -282,7 +282,8 @@ def bench_read_sweep(r, nbytes, steps, warmup):
     """Every read shape of libullm_bench.so's sweep (1-16 waves per workgroup,
     1-32 1 KiB loads in flight per wave, 1-32 KiB per wave) over rotated
     random buffers of `nbytes`: how far the floor the `floor` leg reports is
-    from the fastest plain read of those bytes this harness can time."""
+    from the fastest plain read of those bytes this harness can time; and
+    torch's reductions over the same buffers for comparison."""
     import ctypes
     torch = r.torch
     bench_lib = ctypes.CDLL(str(ROOT / "ullm-project_amd" / "lib" / "libullm_bench.so"))
@@ -312,9 +313,24 @@ def bench_read_sweep(r, nbytes, steps, warmup):
                     calls = [(lambda b=b, w=w, d=d, c=kib * 1024: call(b, w, d, c)) for b in bufs]
                     _, us, _ = r.time_sweep(calls, steps, warmup)
                     shapes.append((us, w, d, kib))
+    # The vendor's own kernels reading the same buffers: torch's reductions
+    # (one pass over the bytes, a few bytes out), as an outside check on the
+    # floor this harness reports.
+    vendor = {}
+    half = nbytes // 8  # int32 elements in half the bytes
+    dst = torch.empty((half,), dtype=torch.int32, device=r.dev)
+    for name, fn_v in (("torch.sum (f32 view)", lambda b: torch.sum(b.view(torch.float32))),
+                       ("torch.amax (i32)", lambda b: torch.amax(b)),
+                       ("copy_ of half the bytes (read + write)",
+                        lambda b: dst.copy_(b[:half]))):
+        calls = [(lambda b=b, f=fn_v: f(b)) for b in bufs]
+        _, us, mode = r.time_sweep(calls, steps, warmup)
+        vendor[name] = {"us": round(us, 3), "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "timing": mode}
     del bufs
     shapes.sort()
     return {"bytes_per_launch": nbytes, "copies": copies, "shapes": len(shapes),
+            "vendor_reads": vendor,
             "best_us": shapes[0][0], "best_GB_s": nbytes / (shapes[0][0] * 1e-6) / 1e9,
             "worst_us": shapes[-1][0],
             "fastest": [{"us": round(u, 3), "waves": w, "depth": d, "kib_per_wave": k}
