@@ -221,6 +221,8 @@ struct GemmCfg {
   static_assert(LDS <= 160 * 1024, "gfx950 LDS per workgroup");
 };
 
+// Zero scale operands: the compiler emits the unscaled
+// v_mfma_f32_16x16x128_f8f6f4 (fp8 x fp8, format code 0 for both).
 __device__ __forceinline__ f32x4 mfma_fp8_k128(i32x8 a, i32x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0,
                                                           0, 0);
