@@ -186,6 +186,10 @@ TIER_PLAN = {
     (8, 28672, 1024): (("rs", 4, 4, 1), ("rs", 4, 7, 1)),
     # the same with a ragged 16-row tile
     (13, 28672, 1024): (("rs", 4, 4, 1), ("rs", 4, 7, 1)),
+    # groups of 7 with two m-tiles (FP8 too: its activation block exceeds
+    # LDS), the second ragged
+    (20, 28672, 1024): (("rs", 4, 7, 1), ("rs", 4, 7, 1)),
+    (32, 28672, 1024): (("rs", 4, 7, 1), ("rs", 4, 7, 1)),
 }
 
 

@@ -1914,10 +1914,15 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          against 6.4 us, 4096->8192 M=8 6.3-6.6 against 6.9 us (at M=16
 //          and 32 the groups of 2 stay ahead: 6.5 against 7.9, 8.8 against
 //          11.4 us);
-//   seven per CU (AQ4, M <= 16, exactly 7 stripes per CU): 4 waves, groups
-//          of 7, one group per CU instead of 1.75 groups of 4; AQ4
-//          4096->28672 (1792 stripes on 256 CUs) M=8 14.8-15.3 against
-//          15.7-15.8 us, M=16 15.3-16.1 against 16.1-16.4 us.
+//   seven per CU (exactly 7 stripes per CU; AQ4 at every M, FP8 at M > 16,
+//          where its activation block does not fit LDS): 4 waves, groups
+//          of 7, one group per CU instead of 1.75 groups of 4, so each CU
+//          reads the activation block once; 4096->28672 (1792 stripes on
+//          256 CUs) AQ4 M=8 14.8-15.3 against 15.7-15.8 us, M=16 15.3-16.1
+//          against 16.1-16.4, M=20 18.6 against 19.8, M=24 19.0 against
+//          20.3, M=32 22.5 against 23.8 us; FP8 M=20 25.0 against 28.5,
+//          M=24 25.1 against 29.3, M=32 26.9 against 31.3 us (FP8 M = 8 and
+//          16 with the LDS-staged kernel switched off: level).
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
@@ -2063,7 +2068,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
     return nullptr;
   }
   const uint32_t cus = device_cu_count();
-  const RsCfg *c = aq4 && a.m <= 16 && stripes == 7 * cus ? &kRsSeven
+  const RsCfg *c = (aq4 || a.m > 16) && stripes == 7 * cus ? &kRsSeven
                    : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
                    : stripes >= 384  ? (!aq4 ? &kRsMediumFp8
@@ -2101,7 +2106,7 @@ hipError_t launch_rs(Kernel kernel, const RsCfg &C, GemvArgs a,
 // any other combination reports an invalid launch.
 constexpr bool rs_reachable(const RsCfg &c, int mt, int p) {
   return (p == 1 || c.s == 1) &&
-         (mt == 1 || !(&c == &kRsSeven || &c == &kRsMediumPacked || &c == &kRsSmall));
+         (mt == 1 || !(&c == &kRsMediumPacked || &c == &kRsSmall));
 }
 #define ULLM_RS_CASE(K, C)                                                  \
   if (c == &C) {                                                            \
@@ -2114,6 +2119,7 @@ constexpr bool rs_reachable(const RsCfg &c, int mt, int p) {
 template <int MT, int P, int EPI>
 hipError_t launch_fp8_rs(const GemvArgs &a, const RsCfg *c, hipStream_t s) {
   ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsWide)
+  ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsSeven)
   ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsLarge)
   ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsMedium)
   ULLM_RS_CASE(fp8_gemv_rs_kernel, kRsDeepK)
