@@ -432,8 +432,8 @@ def main():
     if args.cpu_seconds <= 0:
         args.cpu_seconds = 0.05
     if args.gpus != 1:
-        print("bench.py measures one GPU only: this build's kernels are "
-              "single-GPU (see DESIGN.md on sharding); run with --gpus 1",
+        print("bench.py measures one GPU only: the kernels run on one GPU "
+              "(a multi-GPU deployment would shard N per GPU); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 

@@ -156,8 +156,9 @@ def test_rust_probe_prints_what_the_cxx_probe_prints(probe):
 
 
 def test_integration_doc_lists_every_binding():
-    """INTEGRATION.md points at the binding file instead of restating it, and
-    names every exported function of the extension."""
+    """The integration guide at the repository root points at the binding
+    file instead of restating it, and names every exported function of the
+    extension."""
     doc = (ROOT / "INTEGRATION.md").read_text()
     assert "rust/ullm-hip-sys/src/linear_bindings.rs" in doc
     _, _, rfuncs = _rust_all()
