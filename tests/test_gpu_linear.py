@@ -221,6 +221,30 @@ def test_gemv_parity_register_staged_tiers(uh, orc, gpu, enc, m, n, k):
                  what=f"{enc} gemv bf16 {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("enc", ["fp8", "aq4"])
+def test_gemv_seven_stripe_groups_strided_rows(uh, orc, gpu, enc):
+    """The 7-stripes-per-CU tier with two m-tiles (the second ragged) reading
+    x as a column slice of a wider buffer; plan checked, then the oracle."""
+    m, n, k = 20, 28672, 1024
+    w = weights(n, k, tag=41)
+    wide = activations_bf16(orc, m, k + 136, tag=m + 320)
+    xb = np.ascontiguousarray(wide[:, 8:8 + k])
+    if enc == "fp8":
+        q, s = orc.fp8_quantize_rows(w)
+        y_ref, _ = orc.fp8_gemv(xb, q, s)
+        lw = uh.LinearWeight.from_fp8(q, s)
+    else:
+        p, s, z = orc.aq4_quantize(w)
+        y_ref, _ = orc.aq4_gemv(xb, p, s, z)
+        lw = uh.LinearWeight.from_aq4(p, s, z)
+    x = to_torch_bf16(wide, gpu)[:, 8:8 + k]
+    assert x.stride(0) == k + 136 and x.data_ptr() % 16 == 0
+    y32 = lw.forward(x, out_dtype=torch.float32)
+    check_gemv_plan(lw, x, y32, ("rs", 4, 7, 1))
+    torch.cuda.synchronize()
+    assert_close(y32.cpu().numpy(), y_ref, what=f"{enc} seven-stripe strided")
+
+
 @pytest.mark.parametrize("m", [4, 8])
 @pytest.mark.parametrize("enc", ["fp8", "aq4"])
 def test_gemv_register_staged_strided_rows(uh, orc, gpu, enc, m):
