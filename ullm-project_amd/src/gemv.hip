@@ -1921,8 +1921,8 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          256 CUs) AQ4 M=8 14.8-15.3 against 15.7-15.8 us, M=16 15.3-16.1
 //          against 16.1-16.4, M=20 18.6 against 19.8, M=24 19.0 against
 //          20.3, M=32 22.5 against 23.8 us; FP8 M=20 25.0 against 28.5,
-//          M=24 25.1 against 29.3, M=32 26.9 against 31.3 us (FP8 M = 8 and
-//          16 with the LDS-staged kernel switched off: level).
+//          M=24 25.1 against 29.3, M=32 26.9 against 31.3 us (FP8 at
+//          M <= 16 keeps the LDS-staged multi-stripe kernel).
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
