@@ -188,6 +188,7 @@ TIER_PLAN = {
     (13, 28672, 1024): (("rs", 4, 4, 1), ("rs", 4, 7, 1)),
     # groups of 7 with two m-tiles (FP8 too: its activation block exceeds
     # LDS), the second ragged
+    (16, 28672, 1024): (("rs", 4, 7, 1), ("rs", 4, 7, 1)),
     (20, 28672, 1024): (("rs", 4, 7, 1), ("rs", 4, 7, 1)),
     (32, 28672, 1024): (("rs", 4, 7, 1), ("rs", 4, 7, 1)),
 }

@@ -1914,15 +1914,17 @@ constexpr MsCfg kFp8Ms{ULLM_FP8_MS_CFG};
 //          against 6.4 us, 4096->8192 M=8 6.3-6.6 against 6.9 us (at M=16
 //          and 32 the groups of 2 stay ahead: 6.5 against 7.9, 8.8 against
 //          11.4 us);
-//   seven per CU (exactly 7 stripes per CU; AQ4 at every M, FP8 at M > 16,
-//          where its activation block does not fit LDS): 4 waves, groups
-//          of 7, one group per CU instead of 1.75 groups of 4, so each CU
-//          reads the activation block once; 4096->28672 (1792 stripes on
+//   seven per CU (exactly 7 stripes per CU; AQ4 at every M, FP8 at M >= 16):
+//          4 waves, groups of 7, one group per CU instead of 1.75 groups
+//          of 4, so each CU reads the activation block once; 4096->28672
+//          (1792 stripes on
 //          256 CUs) AQ4 M=8 14.8-15.3 against 15.7-15.8 us, M=16 15.3-16.1
 //          against 16.1-16.4, M=20 18.6 against 19.8, M=24 19.0 against
 //          20.3, M=32 22.5 against 23.8 us; FP8 M=20 25.0 against 28.5,
-//          M=24 25.1 against 29.3, M=32 26.9 against 31.3 us (FP8 at
-//          M <= 16 keeps the LDS-staged multi-stripe kernel).
+//          M=24 25.1 against 29.3, M=32 26.9 against 31.3 us, M=16 22.0
+//          against 22.5 us for the LDS-staged multi-stripe kernel (which
+//          keeps M <= 12: level at 12, ahead at 8 and 9, 21.6 against 22.1
+//          and 21.4 against 21.8 us).
 // Each is {waves, units per batch, ring depth, stripes per group}.
 struct RsCfg {
   int waves, batch, depth, s;
@@ -2003,7 +2005,10 @@ bool use_ms(const GemvArgs &a, bool vec, int mt, bool aq4) {
     // ... except at M >= 16 on small grids (< 384 stripes), where the
     // register-staged single-stripe tier of 8 waves is ahead (4096 -> 4096
     // M=16 6.46 against 6.66 us).
-    return (a.m >= 8 || stripes <= device_cu_count()) && !(a.m >= 16 && stripes < 384);
+    // ... and at M >= 16 on grids of exactly 7 stripes per CU, where one
+    // register-staged group of 7 per CU reads the activations once per CU.
+    return (a.m >= 8 || stripes <= device_cu_count()) && !(a.m >= 16 && stripes < 384) &&
+           !(a.m >= 16 && stripes == 7 * device_cu_count());
   }
   // AQ4: M <= 2, or runs of 3+ stripes, taking two resident workgroups per
   // CU when the activation block leaves room for two.  (At M = 4 the
@@ -2068,7 +2073,7 @@ const RsCfg *plan_rs(const GemvArgs &a, bool vec, bool aq4) {
     return nullptr;
   }
   const uint32_t cus = device_cu_count();
-  const RsCfg *c = (aq4 || a.m > 16) && stripes == 7 * cus ? &kRsSeven
+  const RsCfg *c = (aq4 || a.m >= 16) && stripes == 7 * cus ? &kRsSeven
                    : stripes >= 4096   ? &kRsWide
                    : stripes >= 1024 ? &kRsLarge
                    : stripes >= 384  ? (!aq4 ? &kRsMediumFp8
